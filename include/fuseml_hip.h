@@ -1,0 +1,172 @@
+/*
+ * fuseml_hip.h — C ABI of the MI355X (gfx950) fused GEMM+epilogue kernel family.
+ *
+ * One call computes, for one fusion group (addmm|mm -> pointwise* -> [row/col
+ * reduction]):
+ *
+ *     acc[m,n]  = sum_k A[m,k] * B[k,n]              (bf16|f16 MFMA, fp32 accumulate)
+ *     v[m,n]    = ops[n_ops-1]( ... ops[0](acc) ...)  (fp32, in registers)
+ *     out[m,n]  = cast(v)                             (one store, optional)
+ *     red[m|n]  = sum / amax / mean of v along N or M (fp32 atomics, optional)
+ *
+ * The entry points replace the reference's kernel-side ABI:
+ *   - fuseml_gemm_epilogue replaces the Triton launch
+ *       `kernel_fn[grid](ptrs..., M, N, K, strides...)`
+ *     at fuseml/codegen/kernel_launcher.py:793-796 and 811-814 (argument layout
+ *     built at kernel_launcher.py:766-785, kernel signature emitted at
+ *     fuseml/codegen/kernel_generator.py:1182-1262), and the cuBLASLt
+ *     `addmm_bias_residual` extension entry point at
+ *     fuseml/codegen/cublas_epilogue.py:355-557 (called at 655-676).
+ *   - fuseml_gemm_epilogue_supported replaces the "can this group be fused"
+ *     decisions of fuseml/passes/topology.py:479-571 (is_compute_bound_gemm) and
+ *     fuseml/codegen/cublas_epilogue.py:166-258 (match_cublas_epilogue): with one
+ *     kernel family the only question left is whether a variant exists.
+ *   - fuseml_last_error replaces the exception text Triton raises through
+ *     EagerFallbackGuard (fuseml/codegen/eager_fallback.py:147-166).
+ *
+ * Conventions
+ *   - All pointers are device pointers owned by the caller (PyTorch's caching
+ *     allocator).  The library allocates nothing and frees nothing.
+ *   - Strides are in ELEMENTS.  A is [M,K] with unit stride along K; B is the
+ *     graph's right operand [K,N] with unit stride along K (the `t(W)` view of an
+ *     nn.Linear weight W[N,K]); `ldb` is its stride along N.
+ *   - Every call is asynchronous on `stream` and captures no host state, so it
+ *     is safe inside HIP graph capture.  Reduction buffers are initialised by a
+ *     fill kernel on the same stream (no hipMemset).
+ *   - Return value: 0 on success, a negative FUSEML_E* code otherwise; the
+ *     message is available from fuseml_last_error() on the calling thread.
+ */
+#ifndef FUSEML_HIP_H_
+#define FUSEML_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FUSEML_ABI_VERSION 1
+
+#define FUSEML_MAX_OPS 16
+#define FUSEML_MAX_OPERANDS 8
+#define FUSEML_MAX_EXTRA_OUT 4
+
+/* Element types (operands, outputs). */
+enum {
+  FUSEML_BF16 = 0,
+  FUSEML_F16 = 1,
+  FUSEML_F32 = 2
+};
+
+/* Epilogue op codes.  The op vocabulary is the reference's supported-op table
+ * (fuseml/passes/graph_cut.py:37-55) plus what addmm's own arguments need. */
+enum {
+  FUSEML_OP_NONE = 0,
+  FUSEML_OP_ADD = 1,        /* v = v + scalar * operand[m,n]   (add.Tensor, addmm bias)   */
+  FUSEML_OP_MUL = 2,        /* v = v * operand[m,n]                                        */
+  FUSEML_OP_RELU = 3,       /* v = v > 0 ? v : 0                                           */
+  FUSEML_OP_GELU_ERF = 4,   /* v = 0.5 v (1 + erf(v / sqrt 2))      gelu approximate=none  */
+  FUSEML_OP_GELU_TANH = 5,  /* v = 0.5 v (1 + tanh(sqrt(2/pi)(v + 0.044715 v^3)))          */
+  FUSEML_OP_SIGMOID = 6,    /* v = 1 / (1 + exp(-v))                                       */
+  FUSEML_OP_SCALE = 7,      /* v = v * scalar                (addmm alpha, mul by scalar)  */
+  FUSEML_OP_ADD_SCALAR = 8, /* v = v + scalar                (add of a Python number)      */
+  FUSEML_OP_STORE = 9,      /* extra[operand][m,n] = cast(v) (escape / intermediate store) */
+  FUSEML_OP_ADD_SELF = 10,  /* v = v + scalar * v            (add(x, x, alpha))            */
+  FUSEML_OP_MUL_SELF = 11   /* v = v * v                     (mul(x, x))                   */
+};
+
+/* Reduction selection (bit mask) — fuseml/codegen/kernel_generator.py:1933-2018. */
+enum {
+  FUSEML_RED_SUM = 1,
+  FUSEML_RED_AMAX = 2,
+  FUSEML_RED_MEAN = 4
+};
+
+/* Error codes. */
+enum {
+  FUSEML_OK = 0,
+  FUSEML_EINVAL = -1,       /* malformed descriptor                                */
+  FUSEML_EUNSUPPORTED = -2, /* valid request with no kernel variant (eager bypass) */
+  FUSEML_EHIP = -3,         /* HIP runtime error at launch                         */
+  FUSEML_EDEVICE = -4       /* current device is not gfx950                        */
+};
+
+typedef struct fuseml_epi_op {
+  int32_t kind;    /* FUSEML_OP_*                                            */
+  int32_t operand; /* operand index (ADD/MUL), extra-output index (STORE)   */
+  float scalar;    /* ADD: operand multiplier (alpha); SCALE/ADD_SCALAR/ADD_SELF */
+  int32_t reserved;
+} fuseml_epi_op;
+
+/* A broadcastable epilogue operand: element (m,n) is at
+ * ptr[m*stride_m + n*stride_n].  A [N] row vector has stride_m = 0, an [M,1]
+ * column has stride_n = 0, a 0-d tensor has both 0, an expanded view keeps its
+ * zero strides.  `extent` is one past the largest element offset reachable,
+ * i.e. (M-1)*stride_m + (N-1)*stride_n + 1 for the group's M,N. */
+typedef struct fuseml_operand {
+  const void* ptr;
+  int64_t stride_m;
+  int64_t stride_n;
+  int64_t extent;
+  int32_t dtype; /* FUSEML_BF16 | FUSEML_F16 | FUSEML_F32 */
+  int32_t reserved;
+} fuseml_operand;
+
+/* A row-major [M,N] output: element (m,n) at ptr[m*ld + n]. */
+typedef struct fuseml_output {
+  void* ptr;
+  int64_t ld;
+  int32_t dtype;
+  int32_t reserved;
+} fuseml_output;
+
+typedef struct fuseml_gemm_desc {
+  int64_t M, N, K;
+  const void* a; /* A[M,K]: element (m,k) at a[m*lda + k]                 */
+  int64_t lda;
+  const void* b; /* B[K,N]: element (k,n) at b[n*ldb + k]  (B = t(W))    */
+  int64_t ldb;
+  int32_t ab_dtype; /* FUSEML_BF16 | FUSEML_F16                          */
+  int32_t n_ops;
+  fuseml_epi_op ops[FUSEML_MAX_OPS];
+  int32_t n_operands;
+  int32_t n_extra;
+  fuseml_operand operands[FUSEML_MAX_OPERANDS];
+  fuseml_output out;                         /* ptr NULL: no tile store       */
+  fuseml_output extra[FUSEML_MAX_EXTRA_OUT]; /* targets of FUSEML_OP_STORE    */
+  int32_t reduce_axis;                       /* 1: over N -> [M]; 0: over M -> [N] */
+  uint32_t reduce_mask;                      /* FUSEML_RED_* bits             */
+  float* reduce_out[3];                      /* fp32 [M] or [N]: sum, amax, mean */
+} fuseml_gemm_desc;
+
+/* Launch the fused kernel for `desc` on `stream` (a hipStream_t; NULL = the
+ * null stream).  Replaces kernel_launcher.py:793-796/811-814 and
+ * cublas_epilogue.py:542-551. */
+int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream);
+
+/* 1 if a kernel variant exists for `desc` (shapes, strides, alignment,
+ * dtypes), 0 if not (reason in fuseml_last_error()).  Touches no device state.
+ * Replaces topology.py:479-571 and cublas_epilogue.py:166-258. */
+int fuseml_gemm_epilogue_supported(const fuseml_gemm_desc* desc);
+
+/* Tile configuration the library would launch for `desc`: writes BM, BN,
+ * waves per workgroup and LDS bytes into cfg[0..3].  Replaces the launch
+ * parameter selection of kernel_launcher.py:134-306 / sram_autotuner.py. */
+int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]);
+
+/* Thread-local text of the last error on this thread ("" if none). */
+const char* fuseml_last_error(void);
+
+/* gcnArchName of `device` (e.g. "gfx950:sramecc+:xnack-") into buf. */
+int fuseml_device_arch(int device, char* buf, int buflen);
+
+/* FUSEML_ABI_VERSION and sizeof(fuseml_gemm_desc), for binding checks. */
+int fuseml_abi_version(void);
+size_t fuseml_desc_size(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FUSEML_HIP_H_ */

@@ -1,0 +1,84 @@
+"""The C-ABI library loads, exports every symbol include/fuseml_hip.h declares,
+and agrees with the Python mirror of its structures (no device calls)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from fuseml_amd import _abi
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "fuseml_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(fuseml_\w+)\s*\(", text, re.M)))
+
+
+def test_library_loads_and_abi_matches():
+    lib = _abi.load_library()
+    assert lib.fuseml_abi_version() == _abi.ABI_VERSION
+    assert lib.fuseml_desc_size() == ctypes.sizeof(_abi.GemmDesc)
+
+
+def test_every_declared_symbol_is_exported():
+    lib = _abi.load_library()
+    declared = _declared_functions()
+    assert set(declared) == set(_abi.EXPORTED_SYMBOLS), declared
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    consts = dict((k, int(v)) for k, v in re.findall(r"(FUSEML_\w+)\s*=\s*(-?\d+)", text))
+    assert consts["FUSEML_OP_ADD"] == _abi.OP_ADD
+    assert consts["FUSEML_OP_MUL_SELF"] == _abi.OP_MUL_SELF
+    for name, code in _abi.OP_CODES.items():
+        assert consts[f"FUSEML_OP_{name.upper()}"] == code, name
+    assert consts["FUSEML_RED_MEAN"] == _abi.RED_MEAN
+    assert consts["FUSEML_EDEVICE"] == _abi.EDEVICE
+    defines = dict(re.findall(r"#define (FUSEML_MAX_\w+) (\d+)", text))
+    assert int(defines["FUSEML_MAX_OPS"]) == _abi.MAX_OPS
+    assert int(defines["FUSEML_MAX_OPERANDS"]) == _abi.MAX_OPERANDS
+    assert int(defines["FUSEML_MAX_EXTRA_OUT"]) == _abi.MAX_EXTRA_OUT
+
+
+def _desc(M=256, N=256, K=64):
+    d = _abi.GemmDesc()
+    d.M, d.N, d.K = M, N, K
+    d.a, d.lda, d.b, d.ldb = 0x10000, K, 0x20000, K
+    d.ab_dtype = _abi.BF16
+    d.out.ptr, d.out.ld, d.out.dtype = 0x30000, N, _abi.BF16
+    return d
+
+
+def test_supported_checks_are_host_only():
+    lib = _abi.load_library()
+    d = _desc()
+    assert lib.fuseml_gemm_epilogue_supported(ctypes.byref(d)) == 1
+    d.K = 60  # not a multiple of 8
+    assert lib.fuseml_gemm_epilogue_supported(ctypes.byref(d)) == 0
+    assert "multiples of 8" in _abi.last_error(lib)
+    d = _desc()
+    d.ab_dtype = _abi.F32
+    assert lib.fuseml_gemm_epilogue_supported(ctypes.byref(d)) == 0
+    assert "MFMA" in _abi.last_error(lib)
+    d = _desc()
+    d.n_ops = 1
+    d.ops[0].kind = _abi.OP_ADD
+    d.ops[0].operand = 0  # no operands declared
+    assert lib.fuseml_gemm_epilogue_supported(ctypes.byref(d)) == 0
+    assert "operand index" in _abi.last_error(lib)
+
+
+def test_tile_config_choice():
+    lib = _abi.load_library()
+    cfg = (ctypes.c_int32 * 4)()
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
+    assert tuple(cfg) == (256, 256, 8, 131072)
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(64, 512, 2048)), cfg) == 0
+    assert tuple(cfg) == (128, 128, 4, 65536)
+    assert cfg[3] <= 160 * 1024  # LDS budget of one gfx950 CU

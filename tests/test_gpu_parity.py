@@ -1,0 +1,248 @@
+"""GPU parity: the HIP kernel family (through the C ABI) against the CPU oracle.
+
+Every case builds seeded bf16/f16 inputs on the CPU, runs one fused launch on
+``cuda:0`` through :class:`fuseml_amd.launcher.HipKernelLauncher` (which calls
+``fuseml_gemm_epilogue``), and compares with ``oracle.gemm_epilogue`` evaluated
+in float64 on the same (exactly representable) input values.
+
+Tolerances (stated by the benchmark contract):
+  * 16-bit tile outputs: ``allclose(out, ref, rtol=2e-2, atol=2e-2)`` against
+    the float64 oracle;
+  * fp32 reductions: ``|red - ref| <= 1e-2 * max(|ref|, ref_abs)`` where
+    ``ref_abs`` is the same reduction of ``|v|`` (the reduction's own scale).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm_epilogue as ora
+from oracle import workloads as ora_w
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 2e-2
+ATOL = 2e-2
+RED_RTOL = 1e-2
+
+
+def _launcher(spec, n_inputs):
+    from fuseml_amd.launcher import HipKernelLauncher
+
+    return HipKernelLauncher(spec, n_inputs)
+
+
+def _spec(**kw):
+    from fuseml_amd.epilogue import EpilogueSpec, EpiOp
+
+    ops = tuple(EpiOp(*o) if isinstance(o, tuple) else EpiOp(o) for o in kw.pop("ops"))
+    return EpilogueSpec(ops=ops, **kw)
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _check_tile(out: torch.Tensor, ref: np.ndarray, what: str = "tile"):
+    got = _np(out)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    bad = ~np.isclose(got, ref, rtol=RTOL, atol=ATOL)
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(
+            f"{what}: {bad.sum()} of {bad.size} mismatches, e.g. "
+            + ", ".join(f"{tuple(i)} got {got[tuple(i)]:.5f} ref {ref[tuple(i)]:.5f}" for i in idx)
+        )
+
+
+def _check_red(out: torch.Tensor, ref: np.ndarray, ref_abs: np.ndarray, what: str):
+    got = _np(out)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    tol = RED_RTOL * np.maximum(np.abs(ref), ref_abs) + 1e-6
+    err = np.abs(got - ref)
+    assert (err <= tol).all(), f"{what}: max err {err.max()} (tol at worst {tol[err.argmax()]})"
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _gemm_inputs(M, N, K, dtype, seed=0):
+    a = torch.randn(M, K, generator=_gen(seed)).to(dtype)
+    w = (torch.randn(N, K, generator=_gen(seed + 1)) / max(K, 1) ** 0.5).to(dtype)
+    return a, w
+
+
+# ---------------------------------------------------------------------------
+# Single-op and chain cases at small, ragged shapes
+# ---------------------------------------------------------------------------
+
+CHAINS = {
+    "bias_gelu": [("add", 0, 1.0), ("gelu_erf", -1, 1.0)],
+    "bias_gelu_tanh": [("add", 0, 1.0), ("gelu_tanh", -1, 1.0)],
+    "bias_relu": [("add", 0, 1.0), ("relu", -1, 1.0)],
+    "sigmoid": [("sigmoid", -1, 1.0)],
+    "bias_residual": [("add", 0, 1.0), ("add", 1, 1.0)],
+    "act_heavy": [("add", 0, 1.0), ("relu", -1, 1.0), ("mul", 1, 1.0), ("sigmoid", -1, 1.0), ("add", 2, 1.0)],
+    "scalars": [("scale", -1, 0.5), ("add_scalar", -1, 0.125), ("add_self", -1, 2.0), ("mul_self", -1, 1.0)],
+    "col_bias_alpha": [("add", 3, -0.5)],
+    "bcast_mul": [("mul", 4, 1.0), ("add", 0, 1.0)],
+}
+
+
+def _operands(M, N, dtype, seed=10):
+    """Operand slots: 0 row bias [N], 1 tile [M,N], 2 row [N], 3 column [M,1], 4 stride-0 expand."""
+    g = _gen(seed)
+    row = (torch.rand(N, generator=g) * 0.2 - 0.1).to(dtype)
+    tile = torch.randn(M, N, generator=g).to(dtype)
+    row2 = (torch.rand(N, generator=g) * 0.06 - 0.03).to(dtype)
+    col = torch.randn(M, 1, generator=g).to(dtype)
+    bc = torch.randn(1, N, generator=g).to(dtype).expand(M, N)
+    return [row, tile, row2, col, bc]
+
+
+SHAPES = [
+    (256, 256, 64),     # one 256-tile, one K stage
+    (512, 512, 1024),   # large-tile variant, several K stages
+    (77, 200, 72),      # ragged M, N and K (K % 64 != 0)
+    (1, 8, 8),          # minimum
+    (300, 1000, 136),   # ragged, N % 4 == 0
+    (130, 257, 48),     # N % 4 != 0: element-wise operand/store path
+]
+
+
+@pytest.mark.parametrize("chain", sorted(CHAINS))
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_chain_parity(chain, shape):
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype)
+    ops = _operands(M, N, dtype)
+    inputs = ops + [a, w.t()]
+    left, right = len(ops), len(ops) + 1
+    steps = CHAINS[chain]
+    spec = _spec(left=left, right=right, ops=steps, out_dtype=dtype)
+    print(f"case chain={chain} shape={shape}", flush=True)
+    out = _launcher(spec, len(inputs))(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], left, right, steps)["tile"]
+    _check_tile(out, ref, f"{chain} {shape}")
+
+
+@pytest.mark.parametrize("axis", [1, 0])
+@pytest.mark.parametrize("shape", [(256, 512, 128), (77, 200, 72), (600, 1030, 64), (513, 130, 40)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_reductions_parity(axis, shape):
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=3)
+    bias = (torch.rand(N, generator=_gen(5)) - 0.5).to(dtype)
+    inputs = [bias, a, w.t()]
+    steps = [("add", 0, 1.0), ("sigmoid", -1, 1.0)]  # sigmoid(0)=0.5 would expose padded elements
+    spec = _spec(left=1, right=2, ops=steps, out_dtype=dtype, store_tile=False,
+                 reductions=("sum", "amax", "mean"), reduce_axis=axis,
+                 reduce_dtypes=(torch.float32,) * 3,
+                 outputs=(("red", "sum"), ("red", "amax"), ("red", "mean")))
+    print(f"case reductions axis={axis} shape={shape}", flush=True)
+    s, mx, mean = _launcher(spec, 3)(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], 1, 2, steps, ("sum", "amax", "mean"), axis)
+    v = ref["tile"]
+    _check_red(s, ref["sum"], np.abs(v).sum(axis=axis), "sum")
+    _check_red(mx, ref["amax"], np.abs(v).max(axis=axis), "amax")
+    _check_red(mean, ref["mean"], np.abs(v).mean(axis=axis), "mean")
+
+
+def test_escape_store_and_tile_with_reductions():
+    """mm -> relu (escapes) -> row sum/amax/mean: the C4 group shape, small."""
+    M, N, K = 320, 640, 256
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=7)
+    steps = [("relu", -1, 1.0), ("store", 0, 1.0)]
+    spec = _spec(left=0, right=1, ops=steps, out_dtype=dtype, store_tile=False,
+                 reductions=("sum", "amax", "mean"), reduce_axis=1,
+                 reduce_dtypes=(torch.float32,) * 3, extra_dtypes=(dtype,),
+                 outputs=(("extra", 0), ("red", "sum"), ("red", "amax"), ("red", "mean")))
+    h, s, mx, mean = _launcher(spec, 2)(a.cuda(), w.t().cuda())
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(a), _np(w.t())], 0, 1, steps, ("sum", "amax", "mean"), 1, n_extra=1)
+    _check_tile(h, ref["extra"][0], "escape tile")
+    v = ref["tile"]
+    _check_red(s, ref["sum"], np.abs(v).sum(1), "sum")
+    _check_red(mx, ref["amax"], np.abs(v).max(1), "amax")
+    _check_red(mean, ref["mean"], np.abs(v).mean(1), "mean")
+
+
+def test_fp16_operands_and_saturation():
+    M, N, K = 128, 256, 64
+    a, w = _gemm_inputs(M, N, K, torch.float16, seed=11)
+    steps = [("scale", -1, 4.0e4)]  # pushes |v| past 65504 -> saturates
+    spec = _spec(left=0, right=1, ops=steps, out_dtype=torch.float16)
+    out = _launcher(spec, 2)(a.cuda(), w.t().cuda())
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(a), _np(w.t())], 0, 1, steps)["tile"]
+    ref_sat = np.clip(ref, -ora.FP16_MAX, ora.FP16_MAX)
+    got = _np(out)
+    assert np.isfinite(got).all()
+    assert (np.abs(got) <= ora.FP16_MAX).all()
+    assert np.allclose(got, ref_sat, rtol=RTOL, atol=ATOL * 4.0e4)
+
+
+def test_k_zero_is_epilogue_of_bias():
+    M, N = 64, 96
+    a = torch.empty(M, 0, dtype=torch.bfloat16)
+    w = torch.empty(N, 0, dtype=torch.bfloat16)
+    bias = torch.linspace(-2, 2, N).to(torch.bfloat16)
+    steps = [("add", 0, 1.0), ("gelu_erf", -1, 1.0)]
+    spec = _spec(left=1, right=2, ops=steps, out_dtype=torch.bfloat16)
+    out = _launcher(spec, 3)(bias.cuda(), a.cuda(), w.t().cuda())
+    torch.cuda.synchronize()
+    ref = np.broadcast_to(ora.gelu_erf(_np(bias)), (M, N))
+    _check_tile(out, ref, "K=0")
+
+
+def test_transposed_and_strided_gemm_operands():
+    """A given K-strided and B given N-contiguous: the launcher re-lays them out."""
+    M, N, K = 192, 320, 96
+    a, w = _gemm_inputs(M, N, K, torch.bfloat16, seed=13)
+    a_t = a.t().contiguous().t()          # stride (1, M): not K-contiguous
+    b_nmajor = w.t().contiguous()         # [K,N] row-major: N-contiguous
+    spec = _spec(left=0, right=1, ops=[("relu",)], out_dtype=torch.bfloat16)
+    out = _launcher(spec, 2)(a_t.cuda(), b_nmajor.cuda())
+    torch.cuda.synchronize()
+    ref = ora.relu(ora.gemm(_np(a), _np(w.t())))
+    _check_tile(out, ref, "relayout")
+
+
+# ---------------------------------------------------------------------------
+# Full-size configurations, checked at sampled rows
+# ---------------------------------------------------------------------------
+
+
+def _sample_rows(M, n=48, seed=0):
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, n)]))
+    return rows
+
+
+def test_c2_full_size_sampled_rows():
+    from fuseml_amd.workloads import c2_mlp_block
+
+    wl = c2_mlp_block()
+    m = wl.model
+    x = wl.inputs[0]
+    W1, b1, W2, b2 = m.linear1.weight, m.linear1.bias, m.linear2.weight, m.linear2.bias
+    g1 = _launcher(_spec(left=1, right=2, ops=[("add", 0, 1.0), ("gelu_erf",)], out_dtype=x.dtype), 3)
+    g2 = _launcher(_spec(left=1, right=2, ops=[("add", 0, 1.0), ("add", 3, 1.0)], out_dtype=x.dtype), 4)
+    xd = x.cuda()
+    h = g1(b1.cuda(), xd, W1.t().cuda())
+    y = g2(b2.cuda(), h, W2.t().cuda(), xd)
+    torch.cuda.synchronize()
+    rows = _sample_rows(x.shape[0])
+    ref = ora_w.transformer_mlp(_np(x), _np(W1), _np(b1), _np(W2), _np(b2), rows=rows)
+    _check_tile(y[torch.as_tensor(rows).cuda()], ref, "C2 block")
+    # h is an exact bf16 round of G1; check it too
+    ref_h = ora.gelu_erf(ora_w.linear(_np(x)[rows], _np(W1), _np(b1)))
+    _check_tile(h[torch.as_tensor(rows).cuda()], ref_h, "C2 G1")
