@@ -1,0 +1,281 @@
+"""Benchmark of the fused MLP-block hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2|C3|C4|C5]
+
+A step is one forward of the workload through the fused HIP kernels (for the
+default C2 MLP block: GEMM1+bias+GELU and GEMM2+bias+residual, two launches of
+the gfx950 kernel family through the C ABI), on synthetic seeded inputs that are
+resident in HBM before timing starts.  W untimed steps, then K timed steps
+bracketed by ``torch.cuda.synchronize()``.  Rank 0 prints one JSON line:
+
+* ``value``/``ms_per_step`` — fused block latency in ms (lower is better);
+* ``roofline`` — the dominant kernel's algorithmic FLOPs per launch divided by
+  its average launch duration, measured with HIP events on the launch stream
+  inside the timed region, against the bf16 dense MFMA peak (every config is
+  MFMA-bound on MI355X: arithmetic intensity 443-2184 FLOP/B vs a ridge of
+  ~315 FLOP/B);
+* ``eager_ms`` / ``speedup_vs_eager`` — the same module run by PyTorch eager on
+  the same GPU (hipBLASLt GEMMs + elementwise kernels);
+* ``cpu_baseline`` — the CPU oracle (numpy float32, ``oracle/workloads.py``)
+  timed on this host on a bounded row sample and scaled to the full batch
+  (reported, not a target).
+
+One GPU only: ``--gpus`` above 1 exits with an explanation.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+import torch  # noqa: E402
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+HBM_PEAK_GBS = 8000.0
+
+WORKLOAD_DESC = {
+    "C2": "MLP block memory_bound bf16: x[16384,1024] -> addmm(1024->4096)+b1 -> GELU -> addmm(4096->1024)+b2 + residual x",
+    "C3": "Activation-heavy bf16: x[16384,1024] -> addmm(1024->4096)+b -> ReLU -> *g[16384,4096] -> Sigmoid -> +row[4096]",
+    "C4": "GEMM + fused row reductions bf16: x[8192,2048] @ W[8192,2048]^T -> ReLU -> tile + row sum/amax/mean fp32",
+    "C5": "Stacked MLP x4 bf16: x[8192,4096], 4 x (addmm(4096->16384)+GELU -> addmm(16384->4096)+b2+residual)",
+}
+
+
+def _parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default="C2", choices=sorted(WORKLOAD_DESC))
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--no-eager", action="store_true", help="skip the eager GPU comparison")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# Fused pipelines: one list of (launcher, arg-builder) per workload
+# ---------------------------------------------------------------------------
+
+
+def _build_pipeline(name: str, wl, dev):
+    from fuseml_amd.epilogue import EpilogueSpec, EpiOp
+    from fuseml_amd.launcher import HipKernelLauncher
+
+    dt = wl.dtype
+    m = wl.model
+    stages = []  # (label, launcher, fn(state)->args, gemm (M,N,K))
+
+    def mlp_block(prefix, blk, gemms):
+        g1 = HipKernelLauncher(EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("gelu_erf")), dt), 3)
+        g2 = HipKernelLauncher(EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("add", 3)), dt), 4)
+        w1t, b1 = blk.linear1.weight.t(), blk.linear1.bias
+        w2t, b2 = blk.linear2.weight.t(), blk.linear2.bias
+        stages.append((f"{prefix}G1 addmm+bias+gelu", g1, lambda s: (b1, s["x"], w1t), "h", gemms[0]))
+        stages.append((f"{prefix}G2 addmm+bias+residual", g2, lambda s: (b2, s["h"], w2t, s["x"]), "x", gemms[1]))
+
+    if name == "C2":
+        mlp_block("", m, wl.gemms)
+    elif name == "C5":
+        for i, blk in enumerate(m.blocks):
+            mlp_block(f"B{i} ", blk, wl.gemms[2 * i: 2 * i + 2])
+    elif name == "C3":
+        lin = m.linear
+        spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("relu"), EpiOp("mul", 3), EpiOp("sigmoid"), EpiOp("add", 4)), dt)
+        g = HipKernelLauncher(spec, 5)
+        stages.append(("addmm+bias+relu*g+sigmoid+row", g,
+                       lambda s: (lin.bias, s["x"], lin.weight.t(), s["g"], m.row), "y", wl.gemms[0]))
+    elif name == "C4":
+        spec = EpilogueSpec(0, 1, (EpiOp("relu"), EpiOp("store", 0)), dt, store_tile=False,
+                            reductions=("sum", "amax", "mean"), reduce_axis=1,
+                            reduce_dtypes=(torch.float32,) * 3, extra_dtypes=(dt,),
+                            outputs=(("extra", 0), ("red", "sum"), ("red", "amax"), ("red", "mean")))
+        g = HipKernelLauncher(spec, 2)
+        wt = m.linear.weight.t()
+        stages.append(("mm+relu+rowsum/amax/mean", g, lambda s: (s["x"], wt), "y", wl.gemms[0]))
+    return stages
+
+
+def _run_pipeline(stages, state, events=None):
+    for i, (_, launcher, args, out_key, _) in enumerate(stages):
+        if events is not None:
+            events[i][0].record()
+        out = launcher(*args(state))
+        if events is not None:
+            events[i][1].record()
+        state[out_key] = out
+    return state
+
+
+def _initial_state(name, wl):
+    st = {"x": wl.inputs[0]}
+    if name == "C3":
+        st["g"] = wl.inputs[1]
+    return st
+
+
+# ---------------------------------------------------------------------------
+# CPU oracle baseline (bounded sample, scaled to the full batch)
+# ---------------------------------------------------------------------------
+
+
+def _cpu_baseline(name, wl, seconds):
+    import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    from oracle import workloads as ora_w
+
+    cores = len(os.sched_getaffinity(0))
+    f32 = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    m = wl.model
+    x = f32(wl.inputs[0])
+    M = x.shape[0]
+    rows = np.arange(min(M, 256))
+    if name in ("C2",):
+        args = (f32(m.linear1.weight), f32(m.linear1.bias), f32(m.linear2.weight), f32(m.linear2.bias))
+        fn = lambda: ora_w.transformer_mlp(x, *args, rows=rows, dtype=np.float32)  # noqa: E731
+    elif name == "C3":
+        g = f32(wl.inputs[1])
+        args = (f32(m.linear.weight), f32(m.linear.bias), g, f32(m.row))
+        fn = lambda: ora_w.activation_heavy(x, *args, rows=rows, dtype=np.float32)  # noqa: E731
+    elif name == "C4":
+        w = f32(m.linear.weight)
+        fn = lambda: ora_w.gemm_row_reductions(x, w, rows=rows, dtype=np.float32)  # noqa: E731
+    else:
+        blocks = [(f32(b.linear1.weight), f32(b.linear1.bias), f32(b.linear2.weight), f32(b.linear2.bias))
+                  for b in m.blocks]
+        rows = np.arange(min(M, 64))
+        fn = lambda: ora_w.stacked_mlp(x, blocks, rows=rows, dtype=np.float32)  # noqa: E731
+    with threadpool_limits(limits=cores):
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+        fn()  # warm-up
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            fn()
+            reps += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        dt = (time.perf_counter() - t0) / reps
+    ms_full = dt * 1e3 * (M / len(rows))
+    return {
+        "value": round(ms_full, 3),
+        "unit": "ms per full-batch forward (extrapolated from a row sample)",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"oracle/workloads.py numpy float32 forward of {len(rows)} of {M} rows, "
+                  f"{reps} repetitions in {dt * reps:.1f} s, scaled by {M / len(rows):.0f}",
+    }
+
+
+# ---------------------------------------------------------------------------
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build runs the fused kernels on a single MI355X "
+              "(rows shard across GPUs with no exchange, so N GPUs run N independent copies). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    from fuseml_amd.workloads import WORKLOADS
+
+    name = args.workload
+    dev = torch.device("cuda:0")
+    wl = WORKLOADS[name]()
+    wl.to(dev)
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    stages = _build_pipeline(name, wl, dev)
+    with torch.no_grad():
+        state = _initial_state(name, wl)
+        for _ in range(args.warmup):
+            _run_pipeline(stages, dict(state))
+        torch.cuda.synchronize()
+
+        events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in stages] for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(args.steps):
+            ev = [events[k][i] for i in range(len(stages))]
+            _run_pipeline(stages, dict(state), ev)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    per_kernel = []
+    for i, (label, _, _, _, gemm) in enumerate(stages):
+        durs = [events[k][i][0].elapsed_time(events[k][i][1]) for k in range(args.steps)]
+        avg = sum(durs) / len(durs)
+        Mg, Ng, Kg = gemm
+        flops = 2.0 * Mg * Ng * Kg
+        per_kernel.append({"kernel": label, "avg_ms": round(avg, 4), "gemm_MNK": [Mg, Ng, Kg],
+                           "tflops": round(flops / (avg * 1e-3) / 1e12, 1)})
+    dom = max(range(len(per_kernel)), key=lambda i: per_kernel[i]["avg_ms"])
+    dk = per_kernel[dom]
+    Mg, Ng, Kg = dk["gemm_MNK"]
+    achieved = 2.0 * Mg * Ng * Kg / (dk["avg_ms"] * 1e-3) / 1e12
+
+    eager_ms = None
+    if not args.no_eager:
+        with torch.no_grad():
+            for _ in range(max(3, args.warmup)):
+                wl.model(*wl.inputs)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                wl.model(*wl.inputs)
+            torch.cuda.synchronize()
+            eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = _cpu_baseline(name, wl, args.cpu_seconds)
+
+    line = {
+        "metric": "fused MLP-block latency (ms), % HBM/MFMA roofline, speedup vs eager",
+        "value": round(ms_per_step, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch.Generator inputs, random-init nn.Linear weights)",
+        "config": {"workload": f"{name}: {WORKLOAD_DESC[name]}", "gemms_MNK": wl.gemms,
+                   "parallelism": "single GPU"},
+        "tflops_per_step": round(wl.flops / (ms_per_step * 1e-3) / 1e12, 1),
+        "eager_ms": None if eager_ms is None else round(eager_ms, 4),
+        "speedup_vs_eager": None if eager_ms is None else round(eager_ms / ms_per_step, 3),
+        "kernels": per_kernel,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dk["kernel"],
+            "achieved": round(achieved, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -34,7 +34,10 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <type_traits>
 
 #include "fuseml_hip.h"
 
@@ -46,12 +49,21 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kBK = 64;                 // K elements per LDS stage
-constexpr int kRowBytes = kBK * 2;      // one LDS row = 64 x 16-bit = 128 bytes
 constexpr int kGroupM = 8;              // tile-row strip height of the tile order
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always reads zero
 constexpr int kRsrcWord3 = 0x00020000;  // buffer descriptor word 3 for gfx9 (32-bit data)
 constexpr float kFp16Max = 65504.0f;
+
+// The kernel reads its descriptor in place from the kernel-argument segment
+// (constant address space, scalar loads) instead of through the by-value
+// parameter, whose address the compiler would otherwise copy to scratch.
+typedef const __attribute__((address_space(4))) fuseml_gemm_desc KDesc;
+
+// Host-derived flags kept in the `reserved` field of operands and outputs.
+constexpr int kFlagVec4 = 1;   // unit stride along N, rows 4-element aligned: 8/16-byte vectors
+constexpr int kFlagStage = 2;  // 16-bit, rows 8-element aligned, 16-byte base: LDS-staged tile
+constexpr int kFlagAux = 4;    // row ([N]) or column ([M]) vector staged as fp32 in LDS slot (bits 8-9)
+constexpr int kAuxSlots = 4;   // vector operands staged per launch
 
 thread_local char g_last_error[512];
 
@@ -67,8 +79,15 @@ void set_error(const char* fmt, ...) {
 // Device helpers
 // ---------------------------------------------------------------------------
 
+// Buffer resource over [p, p + bytes).  Every caller passes wave-uniform
+// values; readfirstlane states that to the compiler, which otherwise may build
+// the descriptor in VGPRs and wrap each buffer access in a waterfall loop.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* q = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), kRsrcWord3);
 }
 
 template <typename T>
@@ -115,13 +134,13 @@ __device__ __forceinline__ int dtype_bytes(int dtype) { return dtype == FUSEML_F
 
 // Load the 4 operand values at (m, n..n+3).  `ok` says the whole run of four is
 // inside [0,M) x [0,N); an invalid run reads zeros through the buffer bound.
-__device__ __forceinline__ void load_operand4(const fuseml_operand& op, int m, int n, bool ok,
-                                              float v[4]) {
+template <typename Op>
+__device__ __forceinline__ void load_operand4(const Op& op, int m, int n, bool ok, float v[4]) {
   const int dt = op.dtype;
   const int eb = dtype_bytes(dt);
   const __amdgpu_buffer_rsrc_t r = make_rsrc(op.ptr, (uint32_t)(op.extent * eb));
   const int64_t base = (int64_t)m * op.stride_m + (int64_t)n * op.stride_n;
-  if (op.stride_n == 1 && op.reserved) {
+  if (op.reserved & kFlagVec4) {
     // Unit stride along N and 4-element aligned rows: one vector load.
     const uint32_t off = ok ? (uint32_t)(base * eb) : kOOB;
     if (dt == FUSEML_F32) {
@@ -156,13 +175,13 @@ __device__ __forceinline__ void load_operand4(const fuseml_operand& op, int m, i
 
 // Store 4 values to (m, n..n+3) of a row-major output; vector store when the
 // output rows are 4-element aligned (o.reserved set by the host).
-__device__ __forceinline__ void store_out4(const fuseml_output& o, int m, int n, int M, int N,
-                                           const float v[4]) {
+template <typename Out>
+__device__ __forceinline__ void store_out4(const Out& o, int m, int n, int M, int N, const float v[4]) {
   if (m >= M || n >= N) return;
   const int64_t base = (int64_t)m * o.ld + n;
   if (o.dtype == FUSEML_F32) {
     float* p = reinterpret_cast<float*>(o.ptr) + base;
-    if (o.reserved) {
+    if (o.reserved & kFlagVec4) {
       *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
     } else {
       for (int e = 0; e < 4 && n + e < N; ++e) p[e] = v[e];
@@ -174,7 +193,7 @@ __device__ __forceinline__ void store_out4(const fuseml_output& o, int m, int n,
   for (int e = 0; e < 4; ++e)
     h[e] = (o.dtype == FUSEML_BF16) ? f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
   uint16_t* p = reinterpret_cast<uint16_t*>(o.ptr) + base;
-  if (o.reserved) {
+  if (o.reserved & kFlagVec4) {
     uint2 w;
     w.x = h[0] | (h[1] << 16);
     w.y = h[2] | (h[3] << 16);
@@ -193,21 +212,116 @@ __device__ __forceinline__ void atomic_max_f32(float* p, float v) {
     atomicMin(reinterpret_cast<unsigned int*>(p), __float_as_uint(v));
 }
 
-__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+// erf(z) ~= z * P(z^2) for |z| <= 3 and +-1 beyond: a least-squares fit of
+// erf(z)/z in z^2 (fuseml_amd/csrc/fit_erf.py), |error| <= 3.3e-5 in float32 —
+// far below 16-bit output resolution.  Only FMAs: no quarter-rate
+// transcendentals in the GELU epilogue.
+constexpr float kErfP0 = 1.128277939e+00f;
+constexpr float kErfP1 = -3.753779452e-01f;
+constexpr float kErfP2 = 1.111961758e-01f;
+constexpr float kErfP3 = -2.519724170e-02f;
+constexpr float kErfP4 = 4.275007755e-03f;
+constexpr float kErfP5 = -5.203029650e-04f;
+constexpr float kErfP6 = 4.228057854e-05f;
+constexpr float kErfP7 = -2.029208421e-06f;
+constexpr float kErfP8 = 4.312568586e-08f;
 
-__device__ __forceinline__ float gelu_tanh(float x) {
-  // sqrt(2/pi) = 0.7978845608...; cubic coefficient 0.044715 (Hendrycks & Gimpel 2016).
-  const float u = 0.79788456080286536f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(u));
+__device__ __forceinline__ float erf_poly(float z) {
+  const float zc = __builtin_amdgcn_fmed3f(z, -3.0f, 3.0f);
+  const float t = zc * zc;
+  float p = fmaf(kErfP8, t, kErfP7);
+  p = fmaf(p, t, kErfP6);
+  p = fmaf(p, t, kErfP5);
+  p = fmaf(p, t, kErfP4);
+  p = fmaf(p, t, kErfP3);
+  p = fmaf(p, t, kErfP2);
+  p = fmaf(p, t, kErfP1);
+  p = fmaf(p, t, kErfP0);
+  return __builtin_amdgcn_fmed3f(zc * p, -1.0f, 1.0f);
 }
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// GELU, approximate='none': x * Phi(x) = 0.5 x (1 + erf(x / sqrt 2)).
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float h = 0.5f * x;
+  return fmaf(h, erf_poly(x * 0.70710678118654752f), h);
+}
+
+// Logistic function from the hardware exp2 and reciprocal (about 1 ulp each).
+__device__ __forceinline__ float sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
+// GELU, approximate='tanh': 0.5 x (1 + tanh(u)) with u = sqrt(2/pi)(x + 0.044715 x^3)
+// (Hendrycks & Gimpel 2016).  Since 0.5 (1 + tanh(u)) = sigmoid(2u), this is
+// x * sigmoid(2u).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  constexpr float kC = 0.79788456080286536f;  // sqrt(2/pi)
+  const float two_u = 2.0f * x * fmaf(kC * 0.044715f, x * x, kC);
+  return x * sigmoid(two_u);
+}
+
+// LDS stage geometry for a K depth of BK 16-bit elements.  A stage row (one row
+// of A or of W) is BK*2 bytes = BK/8 chunks of 16 bytes.  A ds_read_b128 is
+// served 16 lanes at a time across 64 four-byte banks (256 bytes), which hold
+// 256/(BK*2) consecutive rows; XOR-ing the chunk index with
+// (row / rows_per_sweep) % chunks gives the 16 consecutive rows that one
+// fragment read touches 16 distinct 16-byte bank groups (no conflicts).
+template <int BK>
+struct StageGeom {
+  static constexpr int kRowBytes = BK * 2;
+  static constexpr int kChunks = BK / 8;
+  static constexpr int kRowsPerSweep = 256 / kRowBytes;
+  static constexpr int kRowsPerDma = 1024 / kRowBytes;  // rows one wave-wide 16-byte DMA fills
+  static_assert(kRowsPerSweep * kChunks == 16, "swizzle covers one 16-lane bank sweep");
+  __device__ static __forceinline__ int swizzle(int row) { return (row / kRowsPerSweep) & (kChunks - 1); }
+};
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
+// wherever an accumulator array is indexed, so every index is a constant and
+// the arrays stay in registers whatever the unroller decides.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Byte address of 8-byte unit u (four 16-bit elements) of row r in an LDS
+// staging tile with BN columns.  Units are XOR-swizzled by (r & 31), so the 32
+// rows that one ds_read_b64/ds_write_b64 of the accumulator layout touches land
+// in 32 distinct bank pairs, and the two units of an aligned 16-byte chunk stay
+// together (swapped when r is odd).
+template <int BN>
+__device__ __forceinline__ int stage_unit(int r, int u) {
+  return r * (2 * BN) + ((u ^ (r & 31)) << 3);
+}
+
+template <int BN>
+__device__ __forceinline__ int stage_chunk(int r, int c) {  // 16-byte chunk c of row r
+  return r * (2 * BN) + (((2 * c) ^ (r & 31)) & ~1) * 8;
+}
+
+__device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, x.w, x.x, x.y}; }
 
 // Run the epilogue op chain on one 32x32 accumulator block of this lane:
-// v[4g+e] is element (m, nb + 8g + e).  The chain is read from the kernel
-// arguments, so the loop and its switch are uniform (scalar) control flow.
-__device__ __forceinline__ void epilogue_block(const fuseml_gemm_desc& d, f32x16_t& v, int m,
-                                               int nb, int M, int N) {
+// v[4g+e] is element (m, nb + 8g + e), and (r_loc, u0 + 2g) its staging row
+// and unit.  Operand `staged` (if >= 0) is read from the LDS staging tile
+// instead of global memory.  The chain is read from the kernel arguments, so
+// the loop and its switch are uniform (scalar) control flow.
+template <int BN, int AUXLEN>
+__device__ __forceinline__ void epilogue_block(KDesc& d, f32x16_t& v, int m,
+                                               int nb, int M, int N, int staged,
+                                               const char* stg, int r_loc, int u0,
+                                               const float* aux, int m_loc, int n_loc) {
   for (int o = 0; o < d.n_ops; ++o) {
     const int kind = d.ops[o].kind;
     const float sc = d.ops[o].scalar;
@@ -216,10 +330,39 @@ __device__ __forceinline__ void epilogue_block(const fuseml_gemm_desc& d, f32x16
       case FUSEML_OP_ADD:
       case FUSEML_OP_MUL: {
         float x[16];
+        const int fl = d.operands[oi].reserved;
+        if (fl & kFlagAux) {
+          const float* a = aux + ((fl >> 8) & (kAuxSlots - 1)) * AUXLEN;
+          if (d.operands[oi].stride_m == 0) {  // row vector: four runs of 4 columns
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = nb + 8 * g;
-          load_operand4(d.operands[oi], m, n, m < M && n < N, x + 4 * g);
+            for (int g = 0; g < 4; ++g) {
+              const float4 q = *reinterpret_cast<const float4*>(a + n_loc + 8 * g);
+              x[4 * g + 0] = q.x;
+              x[4 * g + 1] = q.y;
+              x[4 * g + 2] = q.z;
+              x[4 * g + 3] = q.w;
+            }
+          } else {  // column vector: one value per row
+            const float q = a[m_loc];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) x[r] = q;
+          }
+        } else if (oi == staged) {
+          const int dt = d.operands[oi].dtype;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const uint2 w = *reinterpret_cast<const uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g));
+            x[4 * g + 0] = elem_to_f32(w.x & 0xffffu, dt);
+            x[4 * g + 1] = elem_to_f32(w.x >> 16, dt);
+            x[4 * g + 2] = elem_to_f32(w.y & 0xffffu, dt);
+            x[4 * g + 3] = elem_to_f32(w.y >> 16, dt);
+          }
+        } else {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int n = nb + 8 * g;
+            load_operand4(d.operands[oi], m, n, m < M && n < N, x + 4 * g);
+          }
         }
         if (kind == FUSEML_OP_ADD) {
 #pragma unroll
@@ -280,25 +423,35 @@ __device__ __forceinline__ void epilogue_block(const fuseml_gemm_desc& d, f32x16
 // The kernel
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int WM, int WN, typename T>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_epilogue_kernel(const fuseml_gemm_desc d) {
-  constexpr int NT = WM * WN * 64;
+template <int BM, int BN, int BK, int S, int WM, int WN, typename T>
+__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
+  KDesc& d = *(KDesc*)(__builtin_amdgcn_kernarg_segment_ptr());
+  using G = StageGeom<BK>;
+  constexpr int NW = WM * WN;  // waves per workgroup
+  constexpr int NT = NW * 64;
   constexpr int TM = BM / WM;  // wave tile rows (m)
   constexpr int TN = BN / WN;  // wave tile cols (n)
   constexpr int NJ = TM / 32;  // 32x32 blocks along m (MFMA "B" operand)
   constexpr int NI = TN / 32;  // 32x32 blocks along n (MFMA "A" operand)
-  constexpr int A_BYTES = BM * kRowBytes;
-  constexpr int STAGE = (BM + BN) * kRowBytes;
-  constexpr int A_LD = BM * 8 / NT;  // 16-byte chunks per thread per A stage
-  constexpr int B_LD = BN * 8 / NT;
+  constexpr int RB = G::kRowBytes;
+  constexpr int A_BYTES = BM * RB;
+  constexpr int STAGE = (BM + BN) * RB;
+  constexpr int A_DMA = BM / (G::kRowsPerDma * NW);  // DMA instructions per wave per stage
+  constexpr int B_DMA = BN / (G::kRowsPerDma * NW);
+  constexpr int LPS = A_DMA + B_DMA;                 // vector-memory ops per thread per stage
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
-  static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "stage loads must divide evenly");
+  static_assert(A_DMA * G::kRowsPerDma * NW == BM && B_DMA * G::kRowsPerDma * NW == BN,
+                "stage rows must split evenly over the waves");
+  static_assert(S >= 2 && LPS * (S - 2) < 64, "pipeline depth");
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  constexpr int AUXLEN = BM > BN ? BM : BN;  // floats per staged vector slot
+  __shared__ __attribute__((aligned(1024))) char smem[S * STAGE + kAuxSlots * AUXLEN * 4];
+  float* aux = reinterpret_cast<float*>(smem + S * STAGE);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN;
   const int wn = wave % WN;
 
@@ -306,230 +459,346 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_epilogue_kernel(const fuseml
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
 
-  // XCD-aware tile order.
+  // One workgroup per tile.  XCD-aware order: the hardware deals workgroups to
+  // the 8 XCDs round-robin (XCD = blockIdx % 8), so each XCD is given a
+  // contiguous range of logical tiles; consecutive logical tiles form
+  // GROUP_M-row column strips, so the tiles an XCD runs at the same time share
+  // A rows and B columns in its L2.
   const int nwg = gridDim.x;
   int lid = blockIdx.x;
   if ((nwg & 7) == 0) lid = (lid & 7) * (nwg >> 3) + (lid >> 3);
-  const int strip = kGroupM * tiles_n;
-  const int first_m = (lid / strip) * kGroupM;
-  const int strip_h = min(tiles_m - first_m, kGroupM);
-  const int pid_m = first_m + (lid % strip) % strip_h;
-  const int pid_n = (lid % strip) / strip_h;
-  const int m0 = pid_m * BM;
-  const int n0 = pid_n * BN;
+  {
+    const int strip = kGroupM * tiles_n;
+    const int first_m = (lid / strip) * kGroupM;
+    const int strip_h = min(tiles_m - first_m, kGroupM);
+    const int pid_m = first_m + (lid % strip) % strip_h;
+    const int pid_n = (lid % strip) / strip_h;
+    const int m0 = pid_m * BM;
+    const int n0 = pid_n * BN;
 
-  // Operand buffer resources (the host guarantees the byte extents fit in 31 bits).
-  const uint32_t a_bytes = (uint32_t)(((int64_t)(M - 1) * d.lda + K) * 2);
-  const uint32_t b_bytes = (uint32_t)(((int64_t)(N - 1) * d.ldb + K) * 2);
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(d.a, a_bytes);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(d.b, b_bytes);
+    // Operand buffer resources (the host guarantees the byte extents fit in 31 bits).
+    const uint32_t a_bytes = (uint32_t)(((int64_t)(M - 1) * d.lda + K) * 2);
+    const uint32_t b_bytes = (uint32_t)(((int64_t)(N - 1) * d.ldb + K) * 2);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(d.a, a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(d.b, b_bytes);
 
-  // Per-thread global chunk coordinates (constant over the K loop).
-  uint32_t a_row_off[A_LD], b_row_off[B_LD];
-  int a_kc[A_LD], b_kc[B_LD];
-  uint32_t a_lds[A_LD], b_lds[B_LD];
-#pragma unroll
-  for (int i = 0; i < A_LD; ++i) {
-    const int c = tid + NT * i;
-    const int row = c >> 3, kc = c & 7;
-    const int gm = m0 + row;
-    a_row_off[i] = gm < M ? (uint32_t)((int64_t)gm * d.lda * 2) : kOOB;
-    a_kc[i] = kc;
-    a_lds[i] = row * kRowBytes + ((kc ^ (row & 7)) << 4);
-  }
-#pragma unroll
-  for (int i = 0; i < B_LD; ++i) {
-    const int c = tid + NT * i;
-    const int row = c >> 3, kc = c & 7;
-    const int gn = n0 + row;
-    b_row_off[i] = gn < N ? (uint32_t)((int64_t)gn * d.ldb * 2) : kOOB;
-    b_kc[i] = kc;
-    b_lds[i] = A_BYTES + row * kRowBytes + ((kc ^ (row & 7)) << 4);
-  }
+    // Global -> LDS DMA.  One wave-wide buffer_load_dwordx4 ... lds writes 64 x 16
+    // bytes contiguously from the LDS base in M0, i.e. kRowsPerDma whole stage
+    // rows.  The swizzle is applied on the source side: the lane whose 16-byte
+    // slot is physical chunk c of row r fetches logical chunk c ^ swizzle(r).
+    // Rows past M (or N) are clamped to the last valid row: they load real data
+    // whose results are never stored and are excluded from every reduction.
+    uint32_t a_off[A_DMA], b_off[B_DMA];
+    int a_k[A_DMA], b_k[B_DMA];
+    static_for<0, A_DMA>([&](auto i) {
+      const int row = (wave + NW * i) * G::kRowsPerDma + lane / G::kChunks;
+      const int kc = (lane % G::kChunks) ^ G::swizzle(row);
+      const int gm = min(m0 + row, M - 1);
+      a_off[i] = (uint32_t)((int64_t)gm * d.lda * 2) + (uint32_t)(kc * 16);
+      a_k[i] = kc * 8;
+    });
+    static_for<0, B_DMA>([&](auto i) {
+      const int row = (wave + NW * i) * G::kRowsPerDma + lane / G::kChunks;
+      const int kc = (lane % G::kChunks) ^ G::swizzle(row);
+      const int gn = min(n0 + row, N - 1);
+      b_off[i] = (uint32_t)((int64_t)gn * d.ldb * 2) + (uint32_t)(kc * 16);
+      b_k[i] = kc * 8;
+    });
+    // Stage `kt` of K into LDS slot `slot`.  A chunk whose k range starts at or
+    // past K reads zeros (K is a multiple of 8, so a chunk is wholly inside or
+    // wholly outside [0,K)).
+    auto load_stage = [&](int kt, int slot) {
+      const int k0 = kt * BK;
+      const uint32_t kb = (uint32_t)(k0 * 2);
+      char* st = smem + slot * STAGE;
+      static_for<0, A_DMA>([&](auto i) {
+        const uint32_t off = (k0 + a_k[i] < K) ? a_off[i] + kb : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ra, (__attribute__((address_space(3))) void*)(st + (wave + NW * i) * G::kRowsPerDma * RB), 16,
+            off, 0, 0, 0);
+      });
+      static_for<0, B_DMA>([&](auto i) {
+        const uint32_t off = (k0 + b_k[i] < K) ? b_off[i] + kb : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb, (__attribute__((address_space(3))) void*)(st + A_BYTES + (wave + NW * i) * G::kRowsPerDma * RB),
+            16, off, 0, 0, 0);
+      });
+    };
 
-  i32x4_t ga[A_LD], gb[B_LD];
-  auto load_tile = [&](int kt) {
-    const int k0 = kt * kBK;
-#pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      const int k = k0 + a_kc[i] * 8;
-      const uint32_t off = (a_row_off[i] != kOOB && k < K) ? a_row_off[i] + (uint32_t)(k * 2) : kOOB;
-      ga[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i) {
-      const int k = k0 + b_kc[i] * 8;
-      const uint32_t off = (b_row_off[i] != kOOB && k < K) ? b_row_off[i] + (uint32_t)(k * 2) : kOOB;
-      gb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
-    }
-  };
-  auto store_tile = [&](int stage) {
-    char* s = smem + stage * STAGE;
-#pragma unroll
-    for (int i = 0; i < A_LD; ++i) *reinterpret_cast<i32x4_t*>(s + a_lds[i]) = ga[i];
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i) *reinterpret_cast<i32x4_t*>(s + b_lds[i]) = gb[i];
-  };
+    f32x16_t acc[NI][NJ];
+    static_for<0, NI>([&](auto i) {
+      static_for<0, NJ>([&](auto j) {
+        static_for<0, 16>([&](auto r) { acc[i][j][(int)r] = 0.0f; });
+      });
+    });
 
-  f32x16_t acc[NI][NJ];
-#pragma unroll
-  for (int i = 0; i < NI; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    const int l32 = lane & 31;
+    const int khalf = lane >> 5;
+    const int swz = G::swizzle(l32);  // == swizzle(row) for every fragment row this lane reads
+    // Fragment row byte offsets inside a stage: rows of W feed MFMA "A", rows of x MFMA "B".
+    const int fa_row = A_BYTES + (wn * TN + l32) * RB;
+    const int fb_row = (wm * TM + l32) * RB;
 
-  // Fragment row offsets inside a stage: rows of W for MFMA "A", rows of x for MFMA "B".
-  const int l32 = lane & 31;
-  const int khalf = lane >> 5;
-  const int swz = lane & 7;  // == row & 7 for every fragment row this lane reads
+    // MFMAs of one stage.  Fragments of k-step ks+1 are read from LDS while the
+    // MFMAs of k-step ks run.
+    constexpr int KS = BK / 16;
+    auto compute = [&](const char* st) {
+      i32x4_t fa[2][NI], fb[2][NJ];
+      auto read_frags = [&](int ks, int buf) {
+        const int chunk = ((2 * ks + khalf) ^ swz) << 4;
+        static_for<0, NI>([&](auto i) {
+          fa[buf][i] = *reinterpret_cast<const i32x4_t*>(st + fa_row + 32 * i * RB + chunk);
+        });
+        static_for<0, NJ>([&](auto j) {
+          fb[buf][j] = *reinterpret_cast<const i32x4_t*>(st + fb_row + 32 * j * RB + chunk);
+        });
+      };
+      read_frags(0, 0);
+      static_for<0, KS>([&](auto ks) {
+        constexpr int cur = decltype(ks)::value & 1;
+        if constexpr (decltype(ks)::value + 1 < KS) read_frags(decltype(ks)::value + 1, cur ^ 1);
+        static_for<0, NI>([&](auto i) {
+          static_for<0, NJ>([&](auto j) { acc[i][j] = mfma32<T>(fa[cur][i], fb[cur][j], acc[i][j]); });
+        });
+      });
+    };
 
-  const int nk = (K + kBK - 1) / kBK;
-  if (nk > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int stage = kt & 1;
-    if (kt + 1 < nk) load_tile(kt + 1);
-    const char* s = smem + stage * STAGE;
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int kc = 2 * ks + khalf;
-      const int chunk = (kc ^ swz) << 4;
-      i32x4_t fa[NI], fb[NJ];
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int row = wn * TN + 32 * i + l32;
-        fa[i] = *reinterpret_cast<const i32x4_t*>(s + A_BYTES + row * kRowBytes + chunk);
+    // S-stage pipeline: stages kt+1 .. kt+S-2 stay in flight while stage kt is
+    // consumed; one barrier per stage both publishes the DMA of stage kt (after
+    // each wave's own vmcnt wait) and retires the slot the next DMA overwrites.
+    const int nk = (K + BK - 1) / BK;
+    static_for<0, S - 1>([&](auto p) {
+      if (p < nk) load_stage(p, p);
+    });
+    int slot = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      const int ahead = min(nk - 1 - kt, S - 2);  // stages issued after kt
+      if (ahead == S - 2) {
+        wait_vmcnt<LPS * (S - 2)>();
+      } else {
+        static_for<0, S - 2>([&](auto q) {
+          if (ahead == q) wait_vmcnt<LPS * q>();
+        });
       }
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int row = wm * TM + 32 * j + l32;
-        fb[j] = *reinterpret_cast<const i32x4_t*>(s + row * kRowBytes + chunk);
+      // A bare s_barrier: __syncthreads() would add a release fence that drains
+      // every in-flight DMA.  The asm statements only stop the compiler from
+      // moving memory accesses across the barrier.
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (kt + S - 1 < nk) {
+        int nslot = slot + S - 1;
+        if (nslot >= S) nslot -= S;
+        load_stage(kt + S - 1, nslot);
       }
-#pragma unroll
-      for (int i = 0; i < NI; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32<T>(fa[i], fb[j], acc[i][j]);
+      compute(smem + slot * STAGE);
+      if (++slot == S) slot = 0;
     }
-    if (kt + 1 < nk) store_tile(stage ^ 1);
+    __syncthreads();  // the epilogue reuses LDS
+
+    // ---------------------------------------------------------------------
+    // Epilogue.  In accumulator block (i,j), register r of this lane holds
+    //   m = m0 + wm*TM + 32j + (lane & 31)
+    //   n = n0 + wn*TN + 32i + 8*(r>>2) + 4*(lane>>5) + (r&3).
+    // That layout spreads each load/store instruction over 32 rows, so 2-D
+    // operands and the output go through an LDS staging tile [BM][BN] of 16-bit
+    // elements, filled and drained by whole-row coalesced 16-byte accesses.
+    // ---------------------------------------------------------------------
+    constexpr int SP = 2 * BN;        // staging row pitch in bytes
+    constexpr int CPR = BN / 8;       // 16-byte chunks per staged row
+    constexpr int RPP = NT / CPR;     // staged rows per cooperative pass
+    static_assert(BM % RPP == 0 && BN % 128 == 0, "staging passes");
+    static_assert(BM * SP <= S * STAGE, "staging tile fits in the pipeline's LDS");
+    char* stg = smem;
+
+    const int mw = m0 + wm * TM + l32;
+    const int nw = n0 + wn * TN + 4 * khalf;
+    const bool row_red = d.reduce_mask != 0 && d.reduce_axis == 1;
+    const bool col_red = d.reduce_mask != 0 && d.reduce_axis == 0;
+    const int crow = tid / CPR;  // cooperative-pass row and chunk of this thread
+    const int cchk = tid % CPR;
+
+    // (1) Stage the epilogue operands in LDS: every vector operand the host gave
+    // an aux slot (as fp32), and the first LDS-eligible 2-D operand of the chain.
+    // All global loads of this phase are in flight together; one barrier.
+    bool any_aux = false;
+    for (int oi = 0; oi < d.n_operands; ++oi) {
+      const int fl = d.operands[oi].reserved;
+      if (!(fl & kFlagAux)) continue;
+      any_aux = true;
+      float* a = aux + ((fl >> 8) & (kAuxSlots - 1)) * AUXLEN;
+      const bool rowv = d.operands[oi].stride_m == 0;
+      const int len = rowv ? BN : BM;
+      const int base = rowv ? n0 : m0;
+      const int lim = rowv ? N : M;
+      const int64_t st = rowv ? d.operands[oi].stride_n : d.operands[oi].stride_m;
+      const int dt = d.operands[oi].dtype;
+      const int eb = dt == FUSEML_F32 ? 4 : 2;
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(d.operands[oi].ptr, (uint32_t)(d.operands[oi].extent * eb));
+      for (int t = tid; t < len; t += NT) {
+        const int idx = base + t;
+        const uint32_t off = idx < lim ? (uint32_t)((int64_t)idx * st * eb) : kOOB;
+        const uint32_t bits = (eb == 4) ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)
+                                        : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+        a[t] = elem_to_f32(bits, dt);
+      }
+    }
+    int staged = -1;
+    for (int o = 0; o < d.n_ops; ++o) {
+      const int k = d.ops[o].kind;
+      if ((k == FUSEML_OP_ADD || k == FUSEML_OP_MUL) && (d.operands[d.ops[o].operand].reserved & kFlagStage)) {
+        staged = d.ops[o].operand;
+        break;
+      }
+    }
+    if (staged >= 0) {
+      const void* optr = d.operands[staged].ptr;
+      const int64_t osm = d.operands[staged].stride_m;
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(optr, (uint32_t)(d.operands[staged].extent * 2));
+      static_for<0, BM / RPP>([&](auto p) {
+        const int rl = p * RPP + crow;
+        const int m = m0 + rl, n = n0 + 8 * cchk;
+        const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * osm + n) * 2) : kOOB;
+        i32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        if (rl & 1) x = swap_halves(x);
+        *reinterpret_cast<i32x4_t*>(stg + stage_chunk<BN>(rl, cchk)) = x;
+      });
+    }
+    if (staged >= 0 || any_aux) __syncthreads();
+
+    // (2) Op chain on every block, in registers; reduction partials.
+    float rs[NJ], rmx[NJ];
+    static_for<0, NJ>([&](auto j) {
+      rs[j] = 0.0f;
+      rmx[j] = -INFINITY;
+    });
+    const bool use_stage_out = d.out.ptr != nullptr && (d.out.reserved & kFlagStage) && !col_red;
+    float* red_sum = reinterpret_cast<float*>(smem);
+    float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
+
+    static_for<0, NI>([&](auto i) {
+      float cs[16], cmx[16];
+      static_for<0, 16>([&](auto r) {
+        cs[r] = 0.0f;
+        cmx[r] = -INFINITY;
+      });
+      static_for<0, NJ>([&](auto j) {
+        const int m = mw + 32 * j;
+        const int nb = nw + 32 * i;
+        const int r_loc = wm * TM + 32 * j + l32;
+        const int u0 = (wn * TN + 32 * i) / 4 + khalf;
+        epilogue_block<BN, AUXLEN>(d, acc[i][j], m, nb, M, N, staged, stg, r_loc, u0, aux,
+                                   r_loc, nb - n0);
+        if (d.out.ptr != nullptr && !use_stage_out) {
+          static_for<0, 4>([&](auto g) {
+            const float x[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                acc[i][j][4 * g + 3]};
+            store_out4(d.out, m, nb + 8 * g, M, N, x);
+          });
+        }
+        // Partial reductions exclude every element outside [0,M) x [0,N) (the
+        // reference lets padded tile elements through, kernel_generator.py:1959-1960,
+        // 1983-1984).
+        if (row_red || col_red) {
+          static_for<0, 16>([&](auto r) {
+            const int n = nb + 8 * (r >> 2) + (r & 3);
+            const bool in = (m < M) && (n < N);
+            const float x = acc[i][j][(int)r];
+            if (row_red && in) {
+              rs[j] += x;
+              rmx[j] = fmaxf(rmx[j], x);
+            }
+            if (col_red && in) {
+              cs[r] += x;
+              cmx[r] = fmaxf(cmx[r], x);
+            }
+          });
+        }
+      });
+      if (col_red) {
+        // Column partials: reduce over the 32 rows held by each half-wave.  Column
+        // reductions never use the staged output, so LDS is free here.
+        static_for<0, 16>([&](auto r) {
+  #pragma unroll
+          for (int sh = 1; sh < 32; sh <<= 1) {
+            cs[r] += __shfl_xor(cs[r], sh);
+            cmx[r] = fmaxf(cmx[r], __shfl_xor(cmx[r], sh));
+          }
+          if (l32 == 0) {
+            const int col = wn * TN + 32 * i + 8 * (r >> 2) + 4 * khalf + (r & 3);
+            red_sum[wm * BN + col] = cs[r];
+            red_max[wm * BN + col] = cmx[r];
+          }
+        });
+      }
+    });
+
+    // (3) Staged output: registers -> LDS (16-bit), then whole-row 16-byte stores.
+    if (use_stage_out) {
+      if (staged >= 0) __syncthreads();  // every wave is done reading the staged operand
+      const bool bf = d.out.dtype == FUSEML_BF16;
+      static_for<0, NI>([&](auto i) {
+        static_for<0, NJ>([&](auto j) {
+          const int r_loc = wm * TM + 32 * j + l32;
+          const int u0 = (wn * TN + 32 * i) / 4 + khalf;
+          static_for<0, 4>([&](auto g) {
+            uint32_t h[4];
+            static_for<0, 4>([&](auto e) {
+              const float x = acc[i][j][4 * g + e];
+              h[e] = bf ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+            });
+            *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
+                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+          });
+        });
+      });
+      __syncthreads();
+      static_for<0, BM / RPP>([&](auto p) {
+        const int rl = p * RPP + crow;
+        const int m = m0 + rl, n = n0 + 8 * cchk;
+        i32x4_t x = *reinterpret_cast<const i32x4_t*>(stg + stage_chunk<BN>(rl, cchk));
+        if (rl & 1) x = swap_halves(x);
+        if (m < M && n < N) {
+          uint16_t* dst = reinterpret_cast<uint16_t*>(d.out.ptr) + (int64_t)m * d.out.ld + n;
+          *reinterpret_cast<i32x4_t*>(dst) = x;
+        }
+      });
+    }
+
+    if (d.reduce_mask == 0) return;
+    if (row_red) {
+      if (use_stage_out) __syncthreads();  // LDS staging tile is being drained
+      // Row partials: the other half-wave holds the other 4-column runs of the same rows.
+      static_for<0, NJ>([&](auto j) {
+        const float s2 = rs[j] + __shfl_xor(rs[j], 32);
+        const float m2 = fmaxf(rmx[j], __shfl_xor(rmx[j], 32));
+        if (lane < 32) {
+          const int row = wm * TM + 32 * j + lane;
+          red_sum[wn * BM + row] = s2;
+          red_max[wn * BM + row] = m2;
+        }
+      });
+    }
     __syncthreads();
-  }
 
-  // ---------------------------------------------------------------------
-  // Epilogue, one 32x32 accumulator block at a time.  In block (i,j),
-  // register r of this lane holds
-  //   m = m0 + wm*TM + 32j + (lane & 31)
-  //   n = n0 + wn*TN + 32i + 8*(r>>2) + 4*(lane>>5) + (r&3)
-  // ---------------------------------------------------------------------
-  const int mw = m0 + wm * TM + l32;
-  const int nw = n0 + wn * TN + 4 * khalf;
-  const bool row_red = d.reduce_mask != 0 && d.reduce_axis == 1;
-  const bool col_red = d.reduce_mask != 0 && d.reduce_axis == 0;
-  float* red_sum = reinterpret_cast<float*>(smem);  // LDS is free after the K loop
-  float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
-
-  float rs[NJ], rmx[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    rs[j] = 0.0f;
-    rmx[j] = -INFINITY;
-  }
-
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    float cs[16], cmx[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      cs[r] = 0.0f;
-      cmx[r] = -INFINITY;
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int m = mw + 32 * j;
-      const int nb = nw + 32 * i;
-      f32x16_t v = acc[i][j];
-      epilogue_block(d, v, m, nb, M, N);
-      if (d.out.ptr != nullptr) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float x[4] = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
-          store_out4(d.out, m, nb + 8 * g, M, N, x);
-        }
+    const int len = row_red ? BM : BN;
+    const int nparts = row_red ? WN : WM;
+    const int base = row_red ? m0 : n0;
+    const int lim = row_red ? M : N;
+    const float inv = 1.0f / (float)(row_red ? N : M);
+    for (int t = tid; t < len; t += NT) {
+      const int idx = base + t;
+      if (idx >= lim) continue;
+      float s = 0.0f, mx = -INFINITY;
+      for (int w = 0; w < nparts; ++w) {
+        s += red_sum[w * len + t];
+        mx = fmaxf(mx, red_max[w * len + t]);
       }
-      // Partial reductions exclude every element outside [0,M) x [0,N) (the
-      // reference lets padded tile elements through, kernel_generator.py:1959-1960,
-      // 1983-1984).
-      if (row_red || col_red) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int n = nb + 8 * (r >> 2) + (r & 3);
-          const bool in = (m < M) && (n < N);
-          const float x = v[r];
-          if (row_red && in) {
-            rs[j] += x;
-            rmx[j] = fmaxf(rmx[j], x);
-          }
-          if (col_red && in) {
-            cs[r] += x;
-            cmx[r] = fmaxf(cmx[r], x);
-          }
-        }
-      }
+      if (d.reduce_mask & FUSEML_RED_SUM) atomicAdd(d.reduce_out[0] + idx, s);
+      if (d.reduce_mask & FUSEML_RED_AMAX) atomic_max_f32(d.reduce_out[1] + idx, mx);
+      if (d.reduce_mask & FUSEML_RED_MEAN) atomicAdd(d.reduce_out[2] + idx, s * inv);
     }
-    if (col_red) {
-      // Column partials: reduce over the 32 rows held by each half-wave.
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-#pragma unroll
-        for (int sh = 1; sh < 32; sh <<= 1) {
-          cs[r] += __shfl_xor(cs[r], sh);
-          cmx[r] = fmaxf(cmx[r], __shfl_xor(cmx[r], sh));
-        }
-        if (l32 == 0) {
-          const int col = wn * TN + 32 * i + 8 * (r >> 2) + 4 * khalf + (r & 3);
-          red_sum[wm * BN + col] = cs[r];
-          red_max[wm * BN + col] = cmx[r];
-        }
-      }
-    }
-  }
 
-  if (row_red) {
-    // Row partials: the other half-wave holds the other 4-column runs of the same rows.
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const float s2 = rs[j] + __shfl_xor(rs[j], 32);
-      const float m2 = fmaxf(rmx[j], __shfl_xor(rmx[j], 32));
-      if (lane < 32) {
-        const int row = wm * TM + 32 * j + lane;
-        red_sum[wn * BM + row] = s2;
-        red_max[wn * BM + row] = m2;
-      }
-    }
-  }
-  if (d.reduce_mask == 0) return;
-  __syncthreads();
-
-  const int len = row_red ? BM : BN;
-  const int nparts = row_red ? WN : WM;
-  const int base = row_red ? m0 : n0;
-  const int lim = row_red ? M : N;
-  const float inv = 1.0f / (float)(row_red ? N : M);
-  for (int t = tid; t < len; t += NT) {
-    const int idx = base + t;
-    if (idx >= lim) continue;
-    float s = 0.0f, mx = -INFINITY;
-    for (int w = 0; w < nparts; ++w) {
-      s += red_sum[w * len + t];
-      mx = fmaxf(mx, red_max[w * len + t]);
-    }
-    if (d.reduce_mask & FUSEML_RED_SUM) atomicAdd(d.reduce_out[0] + idx, s);
-    if (d.reduce_mask & FUSEML_RED_AMAX) atomic_max_f32(d.reduce_out[1] + idx, mx);
-    if (d.reduce_mask & FUSEML_RED_MEAN) atomicAdd(d.reduce_out[2] + idx, s * inv);
   }
 }
 
@@ -547,17 +816,27 @@ __global__ void reduce_fill_kernel(float* sum, float* amax, float* mean, int len
 // ---------------------------------------------------------------------------
 
 struct TileConfig {
-  int bm, bn, wm, wn;
+  int bm, bn, bk, stages, wm, wn;
+  constexpr int lds_bytes() const {
+    return stages * (bm + bn) * bk * 2 + kAuxSlots * (bm > bn ? bm : bn) * 4;
+  }
 };
 
-constexpr TileConfig kLarge = {256, 256, 2, 4};  // 8 waves, 128 KB LDS
-constexpr TileConfig kSmall = {128, 128, 2, 2};  // 4 waves,  64 KB LDS
+constexpr TileConfig kLarge = {256, 256, 32, 4, 2, 4};  // 8 waves, 128 KB LDS, 1 workgroup/CU
+constexpr TileConfig kWide = {128, 256, 32, 3, 2, 2};   // 4 waves,  72 KB LDS, 2 workgroups/CU
+constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2};  // 4 waves,  64 KB LDS, 2 workgroups/CU
 
 constexpr int64_t kMaxBytes = (int64_t)1 << 31;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 TileConfig choose_config(const fuseml_gemm_desc& d) {
+  // FUSEML_HIP_TILE=large|wide|small pins a variant (tuning sweeps).
+  if (const char* force = getenv("FUSEML_HIP_TILE")) {
+    if (!strcmp(force, "large")) return kLarge;
+    if (!strcmp(force, "wide")) return kWide;
+    if (!strcmp(force, "small")) return kSmall;
+  }
   // A 256x256 tile keeps the LDS traffic per MFMA low enough for the MFMA pipe
   // to stay busy; below one full wave of 256-tile work the 128x128 variant
   // fills more CUs.
@@ -682,34 +961,48 @@ int validate(const fuseml_gemm_desc* dp) {
   return FUSEML_OK;
 }
 
-// Fill in the host-derived vector-path flags (kept in the `reserved` fields).
+// Fill in the host-derived access-path flags (kept in the `reserved` fields).
 void derive_flags(fuseml_gemm_desc& d) {
   for (int i = 0; i < d.n_operands; ++i) {
     fuseml_operand& op = d.operands[i];
     const int eb = op.dtype == FUSEML_F32 ? 4 : 2;
     const bool vec = op.stride_n == 1 && (op.stride_m % 4 == 0) && (d.N % 4 == 0) &&
                      ((uintptr_t)op.ptr % (4 * eb) == 0);
-    op.reserved = vec ? 1 : 0;
+    const bool stage = eb == 2 && op.stride_n == 1 && op.stride_m != 0 && (op.stride_m % 8 == 0) &&
+                       (d.N % 8 == 0) && ((uintptr_t)op.ptr % 16 == 0);
+    op.reserved = (vec ? kFlagVec4 : 0) | (stage ? kFlagStage : 0);
   }
-  auto out_flag = [&](fuseml_output& o) {
+  // Vector operands of ADD/MUL ops get LDS slots, in first-use order.
+  int slots = 0;
+  for (int o = 0; o < d.n_ops && slots < kAuxSlots; ++o) {
+    const int k = d.ops[o].kind;
+    if (k != FUSEML_OP_ADD && k != FUSEML_OP_MUL) continue;
+    fuseml_operand& op = d.operands[d.ops[o].operand];
+    if ((op.reserved & kFlagAux) || (op.stride_m != 0 && op.stride_n != 0)) continue;
+    op.reserved = (op.reserved & ~kFlagStage) | kFlagAux | (slots << 8);
+    ++slots;
+  }
+  auto out_flags = [&](fuseml_output& o) {
     const int eb = o.dtype == FUSEML_F32 ? 4 : 2;
-    o.reserved = (o.ptr != nullptr && o.ld % 4 == 0 && d.N % 4 == 0 &&
-                  (uintptr_t)o.ptr % (4 * eb) == 0)
-                     ? 1
-                     : 0;
+    const bool vec = o.ptr != nullptr && o.ld % 4 == 0 && d.N % 4 == 0 && (uintptr_t)o.ptr % (4 * eb) == 0;
+    const bool stage = o.ptr != nullptr && eb == 2 && o.ld % 8 == 0 && d.N % 8 == 0 &&
+                       (uintptr_t)o.ptr % 16 == 0;
+    o.reserved = (vec ? kFlagVec4 : 0) | (stage ? kFlagStage : 0);
   };
-  out_flag(d.out);
-  for (int i = 0; i < d.n_extra; ++i) out_flag(d.extra[i]);
+  out_flags(d.out);
+  for (int i = 0; i < d.n_extra; ++i) out_flags(d.extra[i]);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <const TileConfig& C>
 hipError_t launch_variant(const fuseml_gemm_desc& d, hipStream_t stream) {
-  const int64_t tiles = cdiv(d.M, BM) * cdiv(d.N, BN);
-  const dim3 grid((unsigned)tiles), block(WM * WN * 64);
+  const int64_t tiles = cdiv(d.M, C.bm) * cdiv(d.N, C.bn);
+  const dim3 grid((unsigned)tiles), block(C.wm * C.wn * 64);
   if (d.ab_dtype == FUSEML_BF16)
-    hipLaunchKernelGGL((gemm_epilogue_kernel<BM, BN, WM, WN, __bf16>), grid, block, 0, stream, d);
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, __bf16>), grid,
+                       block, 0, stream, d);
   else
-    hipLaunchKernelGGL((gemm_epilogue_kernel<BM, BN, WM, WN, _Float16>), grid, block, 0, stream, d);
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, _Float16>), grid,
+                       block, 0, stream, d);
   return hipGetLastError();
 }
 
@@ -736,7 +1029,7 @@ int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]) {
   cfg[0] = c.bm;
   cfg[1] = c.bn;
   cfg[2] = c.wm * c.wn;
-  cfg[3] = 2 * (c.bm + c.bn) * kRowBytes;
+  cfg[3] = c.lds_bytes();
   return FUSEML_OK;
 }
 
@@ -792,9 +1085,11 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
 
   const TileConfig c = choose_config(d);
   if (c.bm == kLarge.bm && c.bn == kLarge.bn)
-    e = launch_variant<kLarge.bm, kLarge.bn, kLarge.wm, kLarge.wn>(d, stream);
+    e = launch_variant<kLarge>(d, stream);
+  else if (c.bm == kWide.bm && c.bn == kWide.bn)
+    e = launch_variant<kWide>(d, stream);
   else
-    e = launch_variant<kSmall.bm, kSmall.bn, kSmall.wm, kSmall.wn>(d, stream);
+    e = launch_variant<kSmall>(d, stream);
   if (e != hipSuccess) {
     set_error("gemm_epilogue launch: %s", hipGetErrorString(e));
     return FUSEML_EHIP;

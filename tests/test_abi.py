@@ -78,7 +78,8 @@ def test_tile_config_choice():
     lib = _abi.load_library()
     cfg = (ctypes.c_int32 * 4)()
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
-    assert tuple(cfg) == (256, 256, 8, 131072)
+    assert tuple(cfg[:3]) == (256, 256, 8)
+    assert 128 * 1024 <= cfg[3] <= 160 * 1024
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(64, 512, 2048)), cfg) == 0
-    assert tuple(cfg) == (128, 128, 4, 65536)
-    assert cfg[3] <= 160 * 1024  # LDS budget of one gfx950 CU
+    assert tuple(cfg[:3]) == (128, 128, 4)
+    assert 2 * cfg[3] <= 160 * 1024  # two workgroups share one gfx950 CU's LDS
