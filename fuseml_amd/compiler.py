@@ -1,0 +1,226 @@
+"""``FuseMLCompiler`` — the ``torch.compile`` backend, bound to the HIP kernel family.
+
+Usage is the reference's (README.md:48-54)::
+
+    compiled = torch.compile(model, backend=FuseMLCompiler())
+    with torch.no_grad():
+        out = compiled(x)
+
+Pipeline (fuseml/compiler.py:173-437, same entry, same bypass, same
+attributes ``fusion_applied`` / ``fusion_strategy`` / ``fusion_candidates``):
+
+1. ``aot_module_simplified`` lowers the Dynamo graph to ATen.
+2. Pre-scan: no ``addmm``/``mm`` trigger, or none worth fusing under the cost
+   model -> ``_NoFusionPossible`` -> the original ``gm.forward`` is returned
+   (no AOT wrapper on the bypass path, compiler.py:219-228).
+3. :class:`~fuseml_amd.fusion_pass.FuseMLFusionPass` finds the groups and
+   inserts placeholders.
+4. Each placeholder is replaced by :func:`build_hip_launcher` — the HIP
+   launcher wrapped in an eager fallback — or, when no kernel variant fits the
+   group, by the group's eager closure.  A placeholder is never left in the
+   graph (the reference keeps it when a build fails, compiler.py:393-398).
+
+The cost model (replacing topology.py:479-571's NVIDIA tables and the
+Triton/cuBLAS/bypass split) is two-way: the fused HIP kernel when the device
+is gfx950, the operands are bf16/f16, the group fits one launch and its output
+has at least ``min_output_elements`` (the reference's tiny-output rule,
+fusion_pass.py:463 and 498: M*N < 500 000 bypasses), else eager.
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import Any, Callable, Dict, List, Optional, Tuple
+
+import torch
+import torch.fx
+from torch._functorch.aot_autograd import aot_module_simplified, make_boxed_func
+
+from .cache import LauncherCache, launcher_cache_key
+from .epilogue import TRIGGER_TARGETS, UnsupportedGroup, spec_from_group
+from .fusion_group import FusionGroup
+from .fusion_pass import FuseMLFusionPass, fuseml_fused_kernel_placeholder
+
+logger = logging.getLogger("fuseml_amd")
+
+MIN_FUSION_OUTPUT_ELEMENTS = 500_000
+SUPPORTED_GEMM_DTYPES = (torch.bfloat16, torch.float16)
+
+
+class _NoFusionPossible(Exception):
+    """No profitable fusion: return the original forward (no AOT overhead)."""
+
+
+def _meta(node: Any):
+    if not isinstance(node, torch.fx.Node):
+        return None
+    tm = node.meta.get("tensor_meta")
+    if tm is not None and hasattr(tm, "shape"):
+        return tm
+    return node.meta.get("val")
+
+
+def device_is_gfx950(device: Optional[torch.device] = None) -> bool:
+    """True when `device` (default: current) is an MI355X-class gfx950 GPU."""
+    if not torch.cuda.is_available():
+        return False
+    try:
+        idx = torch.cuda.current_device() if device is None or device.index is None else device.index
+        arch = getattr(torch.cuda.get_device_properties(idx), "gcnArchName", "")
+    except Exception:  # pragma: no cover - no device
+        return False
+    return str(arch).startswith("gfx950")
+
+
+def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS) -> Tuple[bool, str]:
+    """Cost model for one addmm/mm trigger: (fuse?, reason)."""
+    if node.target is torch.ops.aten.addmm.default:
+        mat1, mat2 = node.args[1], node.args[2]
+    else:
+        mat1, mat2 = node.args[0], node.args[1]
+    m1, m2, out = _meta(mat1), _meta(mat2), _meta(node)
+    if m1 is None or m2 is None or out is None:
+        return False, "no shape metadata"
+    if len(m1.shape) != 2 or len(m2.shape) != 2:
+        return False, "GEMM operands are not 2-D"
+    if m1.dtype not in SUPPORTED_GEMM_DTYPES or m2.dtype != m1.dtype:
+        return False, f"GEMM dtype {m1.dtype}: no MFMA variant (bf16/f16 only)"
+    M, K = int(m1.shape[0]), int(m1.shape[1])
+    N = int(m2.shape[1])
+    if M * N < min_output_elements:
+        return False, f"tiny output {M}x{N}"
+    if K % 8 != 0:
+        return False, f"K={K} is not a multiple of 8"
+    return True, "fused"
+
+
+def build_hip_launcher(group: FusionGroup, eager_fn: Optional[Callable[..., Any]] = None):
+    """FusionGroup -> HipKernelLauncher (eager fallback attached), or None.
+
+    Replaces compiler.py:443-585 (``_build_launcher``) and 591-630
+    (``_build_cublas_launcher``): the epilogue spec is derived from the
+    group's nodes, arguments and kwargs; a group the kernel family cannot
+    express returns None and the caller installs the eager closure.
+    """
+    from .launcher import HipKernelLauncher
+
+    try:
+        spec = spec_from_group(group)
+    except UnsupportedGroup as exc:
+        logger.info("group %s stays eager: %s", group, exc)
+        return None
+    if eager_fn is None and group.eager_module is not None:
+        eager_fn = group.eager_module
+    return HipKernelLauncher(spec, len(group.inputs), eager_fn=eager_fn,
+                             kernel_signature=f"{group!r}: {spec.describe()}")
+
+
+class _EagerGroup:
+    """Callable running a group's original nodes (no fused kernel)."""
+
+    def __init__(self, module: torch.fx.GraphModule) -> None:
+        self.__name__ = "fuseml_eager_group"
+        self._module = module
+
+    def __call__(self, *args):
+        return self._module(*args)
+
+
+class FuseMLCompiler:
+    """``torch.compile`` backend fusing addmm/mm epilogue chains into HIP kernels."""
+
+    def __init__(self, registry: Any = None, *, fuse_sibling_reductions: bool = False,
+                 min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
+                 require_gfx950: bool = True) -> None:
+        self.registry = registry
+        self.fuse_sibling_reductions = fuse_sibling_reductions
+        self.min_output_elements = min_output_elements
+        self.require_gfx950 = require_gfx950
+        self.fusion_candidates: List[torch.fx.Node] = []
+        self.fusion_applied: bool = False
+        self.fusion_strategy: str = "none"
+        self.launchers: List[Any] = []
+        self._cache = LauncherCache()
+
+    # ------------------------------------------------------------------
+    def __call__(self, gm: torch.fx.GraphModule, example_inputs: List[torch.Tensor]) -> Callable:
+        def _aten_compiler(aten_gm: torch.fx.GraphModule, aten_inputs: List[torch.Tensor]):
+            return make_boxed_func(self._compile_aten_graph(aten_gm, aten_inputs))
+
+        try:
+            return aot_module_simplified(gm, example_inputs, fw_compiler=_aten_compiler)
+        except _NoFusionPossible as exc:
+            self.fusion_applied = False
+            self.fusion_strategy = "none"
+            logger.info("bypassing AOT lowering — %s", exc)
+            return gm.forward
+
+    # ------------------------------------------------------------------
+    def _device_ok(self, inputs: List[Any]) -> bool:
+        if not self.require_gfx950:
+            return True
+        devs = {t.device for t in inputs if isinstance(t, torch.Tensor)}
+        cuda = [d for d in devs if d.type == "cuda"]
+        return bool(cuda) and all(device_is_gfx950(d) for d in cuda)
+
+    def _compile_aten_graph(self, gm: torch.fx.GraphModule, example_inputs: List[Any]) -> Callable:
+        self.fusion_candidates = []
+        if not self._device_ok(example_inputs):
+            raise _NoFusionPossible("inputs are not on a gfx950 GPU")
+        has_trigger = False
+        fusible = False
+        for node in gm.graph.nodes:
+            if node.op == "call_function" and node.target in TRIGGER_TARGETS:
+                has_trigger = True
+                ok, why = trigger_is_fusible(node, self.min_output_elements)
+                node.meta["fuseml_cost_model"] = why
+                if ok:
+                    fusible = True
+                    self.fusion_candidates.append(node)
+        if not has_trigger:
+            raise _NoFusionPossible("no addmm/mm trigger in graph")
+        if not fusible:
+            raise _NoFusionPossible("every trigger is below the fusion threshold or unsupported")
+
+        fpass = FuseMLFusionPass(gm, self.registry, fuse_sibling_reductions=self.fuse_sibling_reductions)
+        gm = fpass.run(example_inputs)
+        placeholders = [n for n in gm.graph.nodes
+                        if n.op == "call_function" and n.target is fuseml_fused_kernel_placeholder]
+        if not placeholders:
+            raise _NoFusionPossible("fusion pass found no fusible sequence")
+
+        strategies = set()
+        for ph in placeholders:
+            group: FusionGroup = ph.meta["fusion_group"]
+            # the pre-scan's verdict (the base node's args are gone after surgery)
+            ok = group.base_node.meta.get("fuseml_cost_model") == "fused"
+            launcher = None
+            if ok:
+                key = launcher_cache_key(group)
+                launcher = self._cache.lookup(key) if key is not None else None
+                if launcher is None:
+                    launcher = build_hip_launcher(group)
+                    if launcher is not None and key is not None:
+                        self._cache.store(key, launcher)
+            if launcher is None:
+                target: Callable = _EagerGroup(group.eager_module)
+                strategies.add("eager")
+            else:
+                target = launcher
+                strategies.add("hip")
+                self.launchers.append(launcher)
+            with gm.graph.inserting_after(ph):
+                new = gm.graph.call_function(target, args=ph.args)
+            new.meta.update({k: v for k, v in ph.meta.items() if k != "fusion_group"})
+            ph.replace_all_uses_with(new)
+            gm.graph.erase_node(ph)
+
+        gm.graph.eliminate_dead_code()
+        gm.recompile()
+        self.fusion_applied = "hip" in strategies
+        self.fusion_strategy = "hip" if strategies == {"hip"} else ("mixed" if self.fusion_applied else "eager")
+        return gm.forward
+
+    @property
+    def cache(self) -> LauncherCache:
+        return self._cache

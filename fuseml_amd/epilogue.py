@@ -277,6 +277,15 @@ def spec_from_group(group: Any) -> EpilogueSpec:
     names = [n for n, _ in reductions]
     if len(set(names)) != len(names):
         raise UnsupportedGroup("duplicate reduction kind in one group")
+    # A reduced value that also escapes (sibling-reduction groups) is written
+    # as the primary tile, which takes the coalesced staged-store path.
+    if reductions and escapes and ops and ops[-1].kind == "store" and ops[-1].operand == len(escapes) - 1 \
+            and escapes[-1] is tile_node:
+        ops.pop()
+        store_tile = True
+        k = len(escapes) - 1
+        outputs = [("tile",) if o == ("extra", k) else o for o in outputs]
+        tile_dtype = extra_dtypes.pop()
     return EpilogueSpec(
         left=left,
         right=right,

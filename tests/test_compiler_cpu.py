@@ -1,0 +1,150 @@
+"""FuseMLCompiler backend plumbing on the CPU (no kernel launches).
+
+* Without a gfx950 device the backend bypasses (the reference's
+  _NoFusionPossible path, fuseml/compiler.py:219-228): the original forward
+  runs and ``fusion_applied`` is False.
+* With the device check disabled and the launcher factory replaced by a
+  recorder, the whole pipeline — AOT lowering, cost model, discovery, surgery,
+  launcher binding — runs and the compiled module still equals eager.
+* A group the kernel family cannot express gets its eager closure: no
+  placeholder is ever left in the graph.
+"""
+
+import pytest
+import torch
+import torch.nn as nn
+
+import fuseml_amd.compiler as comp
+from fuseml_amd.compiler import FuseMLCompiler, trigger_is_fusible
+from fuseml_amd.workloads import ActivationHeavy, GemmRowReductions, TransformerMLP
+
+BF = torch.bfloat16
+
+
+def _compile(model, backend):
+    torch._dynamo.reset()
+    return torch.compile(model, backend=backend)
+
+
+def test_bypass_without_gfx950():
+    torch.manual_seed(0)
+    m = TransformerMLP(64, 256).eval()
+    x = torch.randn(32, 64)
+    be = FuseMLCompiler()
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+        ref = m(x)
+    assert torch.allclose(out, ref)
+    assert be.fusion_applied is False and be.fusion_strategy == "none"
+
+
+class Recorded:
+    """Launcher stand-in: runs the group's eager module and records the spec."""
+
+    built = []
+
+    def __init__(self, group):
+        from fuseml_amd.epilogue import spec_from_group
+
+        self.__name__ = "fuseml_fused_kernel"
+        self.spec = spec_from_group(group)
+        self.module = group.eager_module
+        Recorded.built.append(self)
+
+    def __call__(self, *args):
+        return self.module(*args)
+
+
+@pytest.fixture
+def recorded(monkeypatch):
+    Recorded.built = []
+    monkeypatch.setattr(comp, "build_hip_launcher", lambda group, eager_fn=None: Recorded(group))
+    return Recorded
+
+
+def test_full_pipeline_bf16_mlp(recorded):
+    torch.manual_seed(0)
+    m = TransformerMLP(64, 256).to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+        ref = m(x)
+    assert torch.allclose(out.float(), ref.float(), atol=1e-2)
+    assert be.fusion_applied and be.fusion_strategy == "hip"
+    assert [s.spec.describe() for s in recorded.built] == [
+        "gemm(1,2) -> add[0] -> gelu_erf", "gemm(1,2) -> add[0] -> add[3]"]
+
+
+def test_full_pipeline_sibling_reductions(recorded):
+    torch.manual_seed(0)
+    m = GemmRowReductions(64, 128).to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0, fuse_sibling_reductions=True)
+    with torch.no_grad():
+        got = _compile(m, be)(x)
+        ref = m(x)
+    for a, b in zip(got, ref):
+        assert torch.allclose(a.float(), b.float(), atol=1e-2)
+    assert len(recorded.built) == 1 and recorded.built[0].spec.reductions == ("sum", "amax", "mean")
+
+
+def test_tiny_output_bypasses(recorded):
+    m = TransformerMLP(64, 256).to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)   # 32 x 256 < 500 000 outputs
+    be = FuseMLCompiler(require_gfx950=False)
+    with torch.no_grad():
+        _compile(m, be)(x)
+    assert be.fusion_applied is False and recorded.built == []
+
+
+def test_fp32_gemm_bypasses(recorded):
+    m = TransformerMLP(64, 256).eval()
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        _compile(m, be)(torch.randn(32, 64))
+    assert be.fusion_applied is False and recorded.built == []
+
+
+def test_unbuildable_group_runs_eager(monkeypatch):
+    monkeypatch.setattr(comp, "build_hip_launcher", lambda group, eager_fn=None: None)
+    torch.manual_seed(0)
+    m = ActivationHeavy(64, 256).to(BF).eval()
+    x, g = torch.randn(32, 64, dtype=BF), torch.rand(32, 256, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        out = _compile(m, be)(x, g)
+        ref = m(x, g)
+    assert torch.allclose(out.float(), ref.float(), atol=1e-2)
+    assert be.fusion_applied is False and be.fusion_strategy == "eager"
+
+
+def test_cache_hits_on_identical_blocks(recorded):
+    from fuseml_amd.workloads import StackedMLP
+
+    torch.manual_seed(0)
+    m = StackedMLP(64, 256, 3).to(BF).eval()
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        _compile(m, be)(torch.randn(32, 64, dtype=BF))
+    # three identical blocks: one launcher per distinct (chain, layout), reused by the others
+    assert (be.cache.misses, be.cache.hits, len(be.cache)) == (2, 4, 2)
+    assert len(be.launchers) == 6 and len({id(x) for x in be.launchers}) == 2
+
+
+def test_cost_model_rules():
+    import torch.fx as fx
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    def f(x, w):
+        return torch.mm(x, w)
+
+    gm = make_fx(f)(torch.randn(1024, 64, dtype=BF), torch.randn(64, 1024, dtype=BF))
+    mm = [n for n in gm.graph.nodes if n.op == "call_function"][0]
+    assert trigger_is_fusible(mm)[0]
+    gm2 = make_fx(f)(torch.randn(16, 64, dtype=BF), torch.randn(64, 16, dtype=BF))
+    mm2 = [n for n in gm2.graph.nodes if n.op == "call_function"][0]
+    assert trigger_is_fusible(mm2) == (False, "tiny output 16x16")
+    gm3 = make_fx(f)(torch.randn(1024, 60, dtype=BF), torch.randn(60, 1024, dtype=BF))
+    mm3 = [n for n in gm3.graph.nodes if n.op == "call_function"][0]
+    assert trigger_is_fusible(mm3)[0] is False

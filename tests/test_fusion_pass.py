@@ -1,0 +1,210 @@
+"""Group formation and graph surgery (CPU; structure pinned like the reference's
+tests/test_pattern_matching.py, test_graph_surgery.py and test_shape_propagation.py)."""
+
+import operator
+
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.fx.experimental.proxy_tensor import make_fx
+
+from fuseml_amd.epilogue import spec_from_group
+from fuseml_amd.fusion_pass import FuseMLFusionPass, fuseml_fused_kernel_placeholder
+from fuseml_amd.workloads import ActivationHeavy, GemmRowReductions, StackedMLP, TransformerMLP
+
+aten = torch.ops.aten
+
+
+def trace(model, *inputs):
+    with torch.no_grad():
+        return make_fx(model)(*inputs)
+
+
+def run_pass(model, inputs, **kw):
+    gm = trace(model, *inputs)
+    p = FuseMLFusionPass(gm, **kw)
+    out = p.run(inputs)
+    return p, out
+
+
+def targets(group):
+    return [n.target for n in group.all_nodes]
+
+
+def placeholders(gm):
+    return [n for n in gm.graph.nodes if n.op == "call_function" and n.target is fuseml_fused_kernel_placeholder]
+
+
+def bind_eager(gm, groups):
+    """Replace each placeholder by its group's eager closure and return gm."""
+    for ph in placeholders(gm):
+        mod = ph.meta["fusion_group"].eager_module
+        ph.target = lambda *a, _m=mod: _m(*a)
+    gm.recompile()
+    return gm
+
+
+X = torch.randn(16, 32)
+
+
+def test_mlp_block_two_groups():
+    m = TransformerMLP(32, 64).eval()
+    p, gm = run_pass(m, (X,))
+    assert [targets(g) for g in p.groups] == [
+        [aten.addmm.default, aten.gelu.default],
+        [aten.addmm.default, aten.add.Tensor],
+    ]
+    assert len(placeholders(gm)) == 2
+    # GEMM2 consumes GEMM1's fused output, not an erased node
+    ph1, ph2 = placeholders(gm)
+    assert ph1 in ph2.args
+    with torch.no_grad():
+        assert torch.allclose(bind_eager(gm, p.groups)(X), m(X), atol=1e-5)
+
+
+def test_inputs_order_and_output_metadata():
+    m = TransformerMLP(32, 64).eval()
+    p, _ = run_pass(m, (X,))
+    g1 = p.groups[0]
+    names = [n.op for n in g1.inputs]
+    assert len(g1.inputs) == 3 and names[1] == "placeholder"  # bias, x, t(W1) in first-appearance order
+    assert g1.inputs[2].target is aten.t.default
+    assert g1.output_metadata["shape"] == (16, 64) and g1.output_metadata["dtype"] == torch.float32
+    assert set(g1.node_args_snapshot) == {n.name for n in g1.all_nodes}
+
+
+def test_gelu_tanh_kwarg_survives_to_spec():
+    m = TransformerMLP(32, 64, approximate="tanh", residual=False).eval()
+    p, _ = run_pass(m, (X,))
+    assert [o.kind for o in spec_from_group(p.groups[0]).ops] == ["add", "gelu_tanh"]
+
+
+def test_activation_heavy_single_group_role_bias():
+    m = ActivationHeavy(32, 64).eval()
+    g = torch.rand(16, 64)
+    p, gm = run_pass(m, (X, g))
+    assert len(p.groups) == 1
+    grp = p.groups[0]
+    assert targets(grp) == [aten.addmm.default, aten.relu.default, aten.mul.Tensor,
+                            aten.sigmoid.default, aten.add.Tensor]
+    spec = spec_from_group(grp)
+    kinds = [(o.kind, o.operand) for o in spec.ops]
+    # bias (addmm arg 0) once, then gate and the trailing row at their chain positions
+    assert kinds == [("add", 0), ("relu", -1), ("mul", 3), ("sigmoid", -1), ("add", 4)]
+    with torch.no_grad():
+        assert torch.allclose(bind_eager(gm, p.groups)(X, g), m(X, g), atol=1e-5)
+
+
+def test_sibling_reductions_off_by_default():
+    m = GemmRowReductions(32, 64).eval()
+    p, _ = run_pass(m, (X,))
+    assert [targets(g) for g in p.groups] == [[aten.mm.default, aten.relu.default]]
+
+
+def test_sibling_reductions_opt_in():
+    m = GemmRowReductions(32, 64).eval()
+    p, gm = run_pass(m, (X,), fuse_sibling_reductions=True)
+    assert len(p.groups) == 1
+    grp = p.groups[0]
+    assert [n.target for n in grp.result_nodes] == [aten.sum.dim_IntList, aten.amax.default,
+                                                    aten.mean.dim, aten.relu.default]
+    spec = spec_from_group(grp)
+    assert spec.reductions == ("sum", "amax", "mean") and spec.reduce_axis == 1
+    assert spec.outputs == (("red", "sum"), ("red", "amax"), ("red", "mean"), ("tile",))
+    assert spec.reduce_dtypes[0] == torch.float32  # sum(dtype=float32)
+    getitems = [n for n in gm.graph.nodes if n.target is operator.getitem]
+    assert len(getitems) == 4
+    with torch.no_grad():
+        got = bind_eager(gm, p.groups)(X)
+        ref = m(X)
+    for a, b in zip(got, ref):
+        assert torch.allclose(a, b, atol=1e-5)
+
+
+def test_stacked_blocks():
+    m = StackedMLP(32, 48, 3).eval()
+    p, gm = run_pass(m, (X,))
+    assert len(p.groups) == 6
+    with torch.no_grad():
+        assert torch.allclose(bind_eager(gm, p.groups)(X), m(X), atol=1e-5)
+
+
+class EscapeModel(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.l = nn.Linear(32, 64)
+
+    def forward(self, x):
+        h = F.linear(x, self.l.weight, self.l.bias)
+        a = torch.relu(h)
+        return torch.sigmoid(a), a.sum()
+
+
+def test_escape_node_returns_tuple():
+    m = EscapeModel().eval()
+    p, gm = run_pass(m, (X,))
+    assert len(p.groups) == 0 or all(len(g) > 1 for g in p.groups)
+    # relu has two users (sigmoid and sum): absorption stops at relu
+    g = p.groups[0]
+    assert targets(g) == [aten.addmm.default, aten.relu.default]
+    with torch.no_grad():
+        got = bind_eager(gm, p.groups)(X)
+        ref = m(X)
+    assert torch.allclose(got[0], ref[0], atol=1e-5) and torch.allclose(got[1], ref[1], atol=1e-3)
+
+
+class KeepdimModel(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.l = nn.Linear(32, 64, bias=False)
+
+    def forward(self, x):
+        return torch.relu(self.l(x)).sum(-1, keepdim=True)
+
+
+def test_keepdim_reduction_not_absorbed():
+    p, _ = run_pass(KeepdimModel().eval(), (X,))
+    assert [targets(g) for g in p.groups] == [[aten.mm.default, aten.relu.default]]
+
+
+class LoneGemm(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.l = nn.Linear(32, 64)
+
+    def forward(self, x):
+        return self.l(x)
+
+
+def test_lone_trigger_is_not_a_group():
+    p, gm = run_pass(LoneGemm().eval(), (X,))
+    assert p.groups == [] and placeholders(gm) == []
+
+
+def test_placeholder_raises_if_executed():
+    with pytest.raises(RuntimeError, match="must be replaced"):
+        fuseml_fused_kernel_placeholder(torch.zeros(1))
+
+
+class ScalarChain(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.l = nn.Linear(32, 64)
+
+    def forward(self, x, y):
+        h = self.l(x) * 0.5
+        h = h + 0.125
+        h = torch.add(h, y, alpha=-2.0)
+        return h * h
+
+
+def test_scalar_alpha_and_self_ops_spec():
+    y = torch.randn(16, 64)
+    m = ScalarChain().eval()
+    p, gm = run_pass(m, (X, y))
+    spec = spec_from_group(p.groups[0])
+    assert [(o.kind, o.scalar) for o in spec.ops] == [
+        ("add", 1.0), ("scale", 0.5), ("add_scalar", 0.125), ("add", -2.0), ("mul_self", 1.0)]
+    with torch.no_grad():
+        assert torch.allclose(bind_eager(gm, p.groups)(X, y), m(X, y), atol=1e-5)

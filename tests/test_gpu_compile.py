@@ -1,0 +1,149 @@
+"""End to end on the GPU: torch.compile(model, backend=FuseMLCompiler()).
+
+Each workload (BASELINE configs C1-C5; M scaled down so the float64 oracle
+stays fast, every other dimension at full size) is compiled, run under
+no_grad, and compared with the CPU oracle on the same bf16 inputs.  The test
+also asserts that the fused HIP launchers actually ran (no silent eager path).
+Tolerances: tiles rtol/atol 2e-2; fp32 reductions 1e-2 of the reduction scale.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import workloads as ora_w
+
+pytestmark = pytest.mark.gpu
+
+
+def _f64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _compile(model, **kw):
+    from fuseml_amd.compiler import FuseMLCompiler
+
+    torch._dynamo.reset()
+    be = FuseMLCompiler(**kw)
+    return torch.compile(model, backend=be), be
+
+
+def _launches(be):
+    """Kernel launches made by the backend's launchers (a cached launcher counts once)."""
+    uniq = {id(l): l for l in be.launchers}
+    return sum(getattr(l, "launch_count", 0) for l in uniq.values())
+
+
+def _close(got, ref, what):
+    g = _f64(got)
+    bad = ~np.isclose(g, ref, rtol=2e-2, atol=2e-2)
+    assert not bad.any(), f"{what}: {bad.sum()} mismatches, max err {np.abs(g - ref).max()}"
+
+
+def test_c1_fp32_small_is_bypassed():
+    from fuseml_amd.workloads import c1_transformer_mlp_small
+
+    wl = c1_transformer_mlp_small().to("cuda")
+    compiled, be = _compile(wl.model)
+    with torch.no_grad():
+        out = compiled(*wl.inputs)
+        ref = wl.model(*wl.inputs)
+    assert be.fusion_applied is False
+    assert torch.allclose(out, ref)
+
+
+def test_c2_mlp_block_compiled():
+    from fuseml_amd.workloads import c2_mlp_block
+
+    wl = c2_mlp_block(scale=1 / 8).to("cuda")  # x[2048,1024]
+    compiled, be = _compile(wl.model)
+    with torch.no_grad():
+        y = compiled(*wl.inputs)
+        y = compiled(*wl.inputs)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and be.fusion_strategy == "hip"
+    assert len(be.launchers) == 2 and _launches(be) == 4
+    m = wl.model
+    x = wl.inputs[0]
+    ref = ora_w.transformer_mlp(_f64(x), _f64(m.linear1.weight), _f64(m.linear1.bias),
+                                _f64(m.linear2.weight), _f64(m.linear2.bias))
+    _close(y, ref, "C2")
+
+
+def test_c3_activation_heavy_compiled():
+    from fuseml_amd.workloads import c3_activation_heavy
+
+    wl = c3_activation_heavy(scale=1 / 8).to("cuda")
+    compiled, be = _compile(wl.model)
+    with torch.no_grad():
+        y = compiled(*wl.inputs)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and len(be.launchers) == 1 and _launches(be) == 1
+    m = wl.model
+    x, g = wl.inputs
+    ref = ora_w.activation_heavy(_f64(x), _f64(m.linear.weight), _f64(m.linear.bias), _f64(g), _f64(m.row))
+    _close(y, ref, "C3")
+
+
+def test_c4_row_reductions_compiled_with_sibling_fusion():
+    from fuseml_amd.workloads import c4_gemm_row_reductions
+
+    wl = c4_gemm_row_reductions(scale=1 / 8).to("cuda")  # x[1024,2048] -> [1024,8192]
+    compiled, be = _compile(wl.model, fuse_sibling_reductions=True)
+    with torch.no_grad():
+        h, s, mx, mean = compiled(*wl.inputs)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and len(be.launchers) == 1 and _launches(be) == 1
+    ref = ora_w.gemm_row_reductions(_f64(wl.inputs[0]), _f64(wl.model.linear.weight))
+    _close(h, ref["tile"], "C4 tile")
+    a = np.abs(ref["tile"])
+    for got, key, scale in ((s, "sum", a.sum(1)), (mx, "amax", a.max(1)), (mean, "mean", a.mean(1))):
+        assert got.dtype == torch.float32
+        g = _f64(got)
+        assert np.all(np.abs(g - ref[key]) <= 1e-2 * np.maximum(np.abs(ref[key]), scale) + 1e-6), key
+
+
+def test_c4_default_discovery_matches_reference_grouping():
+    from fuseml_amd.workloads import c4_gemm_row_reductions
+
+    wl = c4_gemm_row_reductions(scale=1 / 8).to("cuda")
+    compiled, be = _compile(wl.model)
+    with torch.no_grad():
+        h, s, mx, mean = compiled(*wl.inputs)
+        rh, rs, rmx, rmean = wl.model(*wl.inputs)
+    torch.cuda.synchronize()
+    assert len(be.launchers) == 1  # mm + relu only, reductions stay eager (reference behaviour)
+    assert be.launchers[0].spec.reductions == ()
+    _close(h, _f64(rh), "C4 tile vs eager")
+
+
+def test_c5_stacked_compiled_two_blocks():
+    from fuseml_amd.workloads import c5_stacked_mlp
+
+    wl = c5_stacked_mlp(scale=1 / 16, num_blocks=2).to("cuda")  # x[512,4096]
+    compiled, be = _compile(wl.model)
+    with torch.no_grad():
+        y = compiled(*wl.inputs)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and _launches(be) == 4
+    blocks = [(_f64(b.linear1.weight), _f64(b.linear1.bias), _f64(b.linear2.weight), _f64(b.linear2.bias))
+              for b in wl.model.blocks]
+    rows = np.arange(0, 512, 16)
+    ref = ora_w.stacked_mlp(_f64(wl.inputs[0]), blocks, rows=rows)
+    _close(y[torch.as_tensor(rows).cuda()], ref, "C5")
+
+
+def test_forced_fallback_on_gpu(monkeypatch):
+    from fuseml_amd.fallback import FORCE_FAIL_ENV
+    from fuseml_amd.workloads import c2_mlp_block
+
+    wl = c2_mlp_block(scale=1 / 8).to("cuda")
+    compiled, be = _compile(wl.model)
+    with torch.no_grad():
+        compiled(*wl.inputs)
+        monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+        y = compiled(*wl.inputs)
+        ref = wl.model(*wl.inputs)
+    torch.cuda.synchronize()
+    assert sum(l.fallback_count for l in {id(l): l for l in be.launchers}.values()) == 2
+    assert torch.equal(y, ref)

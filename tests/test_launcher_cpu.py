@@ -1,0 +1,182 @@
+"""HipKernelLauncher host logic with the C entry point replaced by a recorder (CPU).
+
+Pins the launcher's calling convention (the reference's KernelLauncher
+contract, fuseml/codegen/kernel_launcher.py:640-821): arity check, left/right
+operand roles, M/N/K extraction, output allocation, descriptor contents
+(strides, op codes, operand slots, broadcast strides), return order, and the
+eager fallback (forced from the host).  No device call is made.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+from fuseml_amd import _abi
+from fuseml_amd.epilogue import EpilogueSpec, EpiOp
+from fuseml_amd.fallback import FORCE_FAIL_ENV
+from fuseml_amd.launcher import HipKernelLauncher
+
+
+class Recorder:
+    """Stands in for the library: records each descriptor, returns `rc`."""
+
+    def __init__(self, rc=0, msg=b""):
+        self.calls = []
+        self.rc = rc
+        self.msg = msg
+
+    def fuseml_gemm_epilogue(self, desc_ref, stream):
+        d = ctypes.cast(desc_ref, ctypes.POINTER(_abi.GemmDesc)).contents
+        snap = {
+            "M": d.M, "N": d.N, "K": d.K, "lda": d.lda, "ldb": d.ldb, "ab": d.ab_dtype,
+            "ops": [(d.ops[i].kind, d.ops[i].operand, d.ops[i].scalar) for i in range(d.n_ops)],
+            "operands": [(d.operands[i].stride_m, d.operands[i].stride_n, d.operands[i].extent,
+                          d.operands[i].dtype) for i in range(d.n_operands)],
+            "out": (bool(d.out.ptr), d.out.ld, d.out.dtype),
+            "n_extra": d.n_extra, "mask": d.reduce_mask, "axis": d.reduce_axis,
+            "a": d.a, "b": d.b,
+        }
+        self.calls.append(snap)
+        return self.rc
+
+    def fuseml_last_error(self):
+        return self.msg
+
+
+def make(spec, n, rec, eager=None):
+    launcher = HipKernelLauncher(spec, n, eager_fn=eager)
+    launcher._lib = rec
+    return launcher
+
+
+BF = torch.bfloat16
+
+
+def test_descriptor_for_bias_gelu():
+    rec = Recorder()
+    spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("gelu_erf")), BF)
+    b, x, w = torch.randn(48, dtype=BF), torch.randn(32, 64, dtype=BF), torch.randn(48, 64, dtype=BF)
+    out = make(spec, 3, rec)(b, x, w.t())
+    c = rec.calls[0]
+    assert (c["M"], c["N"], c["K"]) == (32, 48, 64)
+    assert c["lda"] == 64 and c["ldb"] == 64           # t(W) is K-contiguous: no copy
+    assert c["b"] == w.data_ptr() and c["a"] == x.data_ptr()
+    assert c["ops"] == [(_abi.OP_ADD, 0, 1.0), (_abi.OP_GELU_ERF, -1, 1.0)]
+    assert c["operands"] == [(0, 1, 48, _abi.BF16)]     # [N] bias broadcast over M
+    assert c["out"] == (True, 48, _abi.BF16) and c["mask"] == 0
+    assert out.shape == (32, 48) and out.dtype == BF and out.is_contiguous()
+
+
+def test_operand_slots_dedupe_and_broadcast_kinds():
+    rec = Recorder()
+    ops = (EpiOp("add", 0), EpiOp("mul", 3), EpiOp("add", 4, 2.0), EpiOp("mul", 0), EpiOp("add", 5))
+    spec = EpilogueSpec(1, 2, ops, BF)
+    M, N, K = 8, 16, 24
+    b = torch.randn(N, dtype=BF)
+    x, wt = torch.randn(M, K, dtype=BF), torch.randn(N, K, dtype=BF).t()
+    tile = torch.randn(M, N, dtype=BF)
+    col = torch.randn(M, 1, dtype=torch.float16)
+    scalar = torch.tensor(3.0)
+    make(spec, 6, rec)(b, x, wt, tile, col, scalar)
+    c = rec.calls[0]
+    # operand 0 appears twice but occupies one slot
+    assert [o[1] for o in c["ops"]] == [0, 1, 2, 0, 3]
+    assert c["operands"][0] == (0, 1, N, _abi.BF16)
+    assert c["operands"][1] == (N, 1, M * N, _abi.BF16)
+    assert c["operands"][2] == (1, 0, M, _abi.F16)           # column vector
+    assert c["operands"][3] == (0, 0, 1, _abi.F32)           # 0-d tensor
+    assert c["ops"][2][2] == 2.0
+
+
+def test_relayout_of_non_k_contiguous_operands():
+    rec = Recorder()
+    spec = EpilogueSpec(0, 1, (EpiOp("relu"),), BF)
+    a = torch.randn(64, 32, dtype=BF).t()           # [32,64] with stride (1,32): not K-contiguous
+    b = torch.randn(64, 40, dtype=BF)               # [K,N] row-major: N-contiguous
+    make(spec, 2, rec)(a, b)
+    c = rec.calls[0]
+    assert (c["M"], c["N"], c["K"]) == (32, 40, 64)
+    assert c["lda"] == 64 and c["ldb"] == 64
+
+
+def test_reductions_and_return_order():
+    rec = Recorder()
+    spec = EpilogueSpec(0, 1, (EpiOp("relu"),), BF, store_tile=True, reductions=("sum", "amax", "mean"),
+                        reduce_axis=1, reduce_dtypes=(torch.float32, BF, torch.float32),
+                        outputs=(("red", "sum"), ("red", "amax"), ("red", "mean"), ("tile",)))
+    s, mx, mean, tile = make(spec, 2, rec)(torch.randn(8, 16, dtype=BF), torch.randn(24, 16, dtype=BF).t())
+    c = rec.calls[0]
+    assert c["mask"] == 7 and c["axis"] == 1
+    assert s.shape == (8,) and s.dtype == torch.float32
+    assert mx.dtype == BF                         # accumulated in fp32, cast to the node's dtype
+    assert tile.shape == (8, 24)
+
+
+def test_arity_error_is_value_error():
+    spec = EpilogueSpec(0, 1, (), BF)
+    with pytest.raises(ValueError, match="Expected 2"):
+        make(spec, 2, Recorder())(torch.randn(4, 8, dtype=BF))
+
+
+def test_negative_stride_detection():
+    """torch never produces negative strides (flip copies); the guard is checked on stubs,
+    as the reference does with fake tensors (tests/test_kernel_launcher.py:379-391)."""
+    from fuseml_amd.launcher import _has_negative_stride
+
+    class Stub:
+        def __init__(self, st):
+            self._st = st
+
+        def stride(self):
+            return self._st
+
+    assert _has_negative_stride(Stub((-24, 1)))
+    assert not _has_negative_stride(Stub((0, 1)))
+    assert not _has_negative_stride(torch.randn(3, 4).t())
+
+
+def test_error_code_raises_runtime_error_without_guard():
+    spec = EpilogueSpec(0, 1, (), BF)
+    launcher = make(spec, 2, Recorder(rc=_abi.EUNSUPPORTED, msg=b"no variant"))
+    with pytest.raises(_abi.FuseMLHipError, match="no variant"):
+        launcher(torch.randn(4, 8, dtype=BF), torch.randn(8, 8, dtype=BF).t())
+
+
+def test_error_code_falls_back_to_eager():
+    spec = EpilogueSpec(0, 1, (EpiOp("relu"),), BF)
+    eager = lambda a, b: torch.relu(a @ b)  # noqa: E731
+    launcher = make(spec, 2, Recorder(rc=_abi.EHIP, msg=b"launch failed"), eager=eager)
+    a, b = torch.randn(4, 8, dtype=BF), torch.randn(8, 8, dtype=BF).t()
+    out = launcher(a, b)
+    assert torch.equal(out, eager(a, b))
+    assert launcher.fallback_count == 1
+
+
+def test_forced_failure_from_host(monkeypatch):
+    rec = Recorder()
+    spec = EpilogueSpec(0, 1, (EpiOp("relu"),), BF)
+    eager = lambda a, b: torch.relu(a @ b)  # noqa: E731
+    launcher = make(spec, 2, rec, eager=eager)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    a, b = torch.randn(4, 8, dtype=BF), torch.randn(8, 8, dtype=BF).t()
+    assert torch.equal(launcher(a, b), eager(a, b))
+    assert rec.calls == [] and launcher.fallback_count == 1
+
+
+def test_value_errors_are_not_swallowed_by_guard():
+    spec = EpilogueSpec(0, 1, (), BF)
+    launcher = make(spec, 2, Recorder(), eager=lambda *a: None)
+    with pytest.raises(ValueError):
+        launcher(torch.randn(4, 8, dtype=BF))
+
+
+def test_unsupported_gemm_dtype_raises():
+    spec = EpilogueSpec(0, 1, (), torch.float32)
+    launcher = make(spec, 2, Recorder())
+    with pytest.raises(_abi.FuseMLHipError, match="bf16/f16"):
+        launcher(torch.randn(4, 8), torch.randn(8, 8).t())
+
+
+def test_name_for_fx():
+    assert HipKernelLauncher(EpilogueSpec(0, 1, (), BF), 2).__name__ == "fuseml_fused_kernel"
