@@ -57,6 +57,8 @@ def _parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--no-eager", action="store_true", help="skip the eager GPU comparison")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--calib-copy-mb", type=int, default=0,
+                   help="after timing, run device copies of this size (rocprof counter calibration)")
     return p.parse_args()
 
 
@@ -93,10 +95,11 @@ def _build_pipeline(name: str, wl, dev):
         stages.append(("addmm+bias+relu*g+sigmoid+row", g,
                        lambda s: (lin.bias, s["x"], lin.weight.t(), s["g"], m.row), "y", wl.gemms[0]))
     elif name == "C4":
-        spec = EpilogueSpec(0, 1, (EpiOp("relu"), EpiOp("store", 0)), dt, store_tile=False,
+        # the spec FuseMLCompiler(fuse_sibling_reductions=True) derives for this module
+        spec = EpilogueSpec(0, 1, (EpiOp("relu"),), dt, store_tile=True,
                             reductions=("sum", "amax", "mean"), reduce_axis=1,
-                            reduce_dtypes=(torch.float32,) * 3, extra_dtypes=(dt,),
-                            outputs=(("extra", 0), ("red", "sum"), ("red", "amax"), ("red", "mean")))
+                            reduce_dtypes=(torch.float32,) * 3,
+                            outputs=(("red", "sum"), ("red", "amax"), ("red", "mean"), ("tile",)))
         g = HipKernelLauncher(spec, 2)
         wt = m.linear.weight.t()
         stages.append(("mm+relu+rowsum/amax/mean", g, lambda s: (s["x"], wt), "y", wl.gemms[0]))
@@ -119,6 +122,44 @@ def _initial_state(name, wl):
     if name == "C3":
         st["g"] = wl.inputs[1]
     return st
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic per launch, from the committed rocprofv3 counter summary
+# ---------------------------------------------------------------------------
+
+TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "traffic_{workload}.md")
+
+
+def _grid_of(launcher, M, N):
+    import ctypes
+
+    from fuseml_amd import _abi
+
+    d = _abi.GemmDesc()
+    d.M, d.N, d.K = M, N, 64
+    d.a, d.lda, d.b, d.ldb = 16, 64, 16, 64
+    d.ab_dtype = _abi.BF16
+    d.out.ptr, d.out.ld, d.out.dtype = 16, N, _abi.BF16
+    cfg = (ctypes.c_int32 * 4)()
+    if launcher._lib.fuseml_gemm_epilogue_config(ctypes.byref(d), cfg) != 0:
+        return None
+    return ((M + cfg[0] - 1) // cfg[0]) * ((N + cfg[1] - 1) // cfg[1]) * cfg[2] * 64
+
+
+def _traffic(workload, grid_threads):
+    """Bytes per launch for the kernel with this grid (threads), or None."""
+    path = TRAFFIC_SUMMARY.format(workload=workload)
+    if grid_threads is None or not os.path.exists(path):
+        return None
+    text = open(path).read()
+    if "```json" not in text:
+        return None
+    data = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    for k in data.get("kernels", []):
+        if k.get("grid") == grid_threads and k.get("fetch_bytes") is not None and k.get("write_bytes") is not None:
+            return int(k["fetch_bytes"] + k["write_bytes"])
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -228,6 +269,15 @@ def main():
     Mg, Ng, Kg = dk["gemm_MNK"]
     achieved = 2.0 * Mg * Ng * Kg / (dk["avg_ms"] * 1e-3) / 1e12
 
+    if args.calib_copy_mb > 0:
+        nbytes = args.calib_copy_mb * 1024 * 1024
+        src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     eager_ms = None
     if not args.no_eager:
         with torch.no_grad():
@@ -270,7 +320,7 @@ def main():
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": _traffic(name, _grid_of(stages[dom][1], Mg, Ng)),
         },
         "cpu_baseline": cpu,
     }

@@ -1,0 +1,109 @@
+"""Summaries of rocprofv3 output for the fused kernels.
+
+    python -m fuseml_amd.profiling trace <kernel_trace.csv>
+    python -m fuseml_amd.profiling traffic <fetch counter_collection.csv> <write counter_collection.csv> \
+        --copy-mib 512
+
+``trace`` groups dispatches by (kernel, grid size) — the G1 and G2 GEMMs of
+one block are the same template at different grids — and prints call count
+and average / min / max duration.
+
+``traffic`` turns the per-dispatch ``FETCH_SIZE`` and ``WRITE_SIZE`` counters
+(KiB) into bytes per launch.  The counters are scaled by what they read for a
+device-to-device copy of known size run in the same process
+(``bench.py --calib-copy-mb``): factor = copy bytes / counter bytes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import statistics
+import sys
+from collections import defaultdict
+from typing import Dict, List, Tuple
+
+COPY_KERNEL_HINT = "copyBuffer"
+
+
+def _short(name: str) -> str:
+    if "gemm_epilogue_kernel" in name:
+        return "gemm_epilogue_kernel" + name[name.index("ILi"):].split("EEv")[0].replace("ILi", "<").replace("ELi", ",")
+    return name[:60]
+
+
+def trace_summary(path: str) -> List[Dict[str, object]]:
+    rows = list(csv.DictReader(open(path)))
+    groups: Dict[Tuple[str, int], List[float]] = defaultdict(list)
+    for r in rows:
+        grid = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0)
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # us
+        groups[(r["Kernel_Name"], grid)].append(dur)
+    out = []
+    for (name, grid), durs in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        out.append({"kernel": _short(name), "grid": grid, "calls": len(durs),
+                    "avg_us": round(statistics.mean(durs), 2), "min_us": round(min(durs), 2),
+                    "max_us": round(max(durs), 2)})
+    return out
+
+
+def counter_by_dispatch(path: str, counter: str) -> Dict[Tuple[str, int], List[float]]:
+    rows = list(csv.DictReader(open(path)))
+    acc: Dict[Tuple[str, int], List[float]] = defaultdict(list)
+    for r in rows:
+        if r["Counter_Name"] != counter:
+            continue
+        acc[(r["Kernel_Name"], int(r.get("Grid_Size") or r.get("Grid_Size_X") or 0))].append(float(r["Counter_Value"]))
+    return acc
+
+
+def traffic_summary(fetch_csv: str, write_csv: str, copy_mib: float) -> Dict[str, object]:
+    fetch = counter_by_dispatch(fetch_csv, "FETCH_SIZE")
+    write = counter_by_dispatch(write_csv, "WRITE_SIZE")
+    copy_bytes = copy_mib * 1024 * 1024
+
+    def copy_factor(table):
+        vals = [v for (n, _), vs in table.items() if COPY_KERNEL_HINT in n for v in vs]
+        big = [v for v in vals if v * 1024 > 0.5 * copy_bytes]
+        if not big:
+            return None
+        return copy_bytes / (statistics.median(big) * 1024)
+
+    ff, wf = copy_factor(fetch), copy_factor(write)
+    kernels = []
+    for key in sorted(set(fetch) | set(write)):
+        name, grid = key
+        if COPY_KERNEL_HINT in name:
+            continue
+        f = statistics.mean(fetch.get(key, [0.0])) * 1024
+        w = statistics.mean(write.get(key, [0.0])) * 1024
+        kernels.append({
+            "kernel": _short(name), "grid": grid,
+            "fetch_bytes_raw": f, "write_bytes_raw": w,
+            "fetch_bytes": None if ff is None else f * ff,
+            "write_bytes": None if wf is None else w * wf,
+        })
+    return {"copy_mib": copy_mib, "fetch_factor": ff, "write_factor": wf, "kernels": kernels}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("csv")
+    tr = sub.add_parser("traffic")
+    tr.add_argument("fetch_csv")
+    tr.add_argument("write_csv")
+    tr.add_argument("--copy-mib", type=float, required=True)
+    a = ap.parse_args(argv)
+    if a.cmd == "trace":
+        for row in trace_summary(a.csv):
+            print(json.dumps(row))
+    else:
+        print(json.dumps(traffic_summary(a.fetch_csv, a.write_csv, a.copy_mib), indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
