@@ -1,4 +1,4 @@
-"""Fit the erf polynomial used by the kernels' GELU (prints the C constants).
+"""Fit the erf polynomial behind the kernels' GELU (prints the C constants).
 
 erf(z) is odd and saturates, so it is approximated on [0, Z] as
     erf(z) ~= z * P(z^2),   P a degree-D polynomial,
@@ -7,6 +7,10 @@ fit (weight z, so the error of erf itself is levelled) on a dense grid,
 computed in a Chebyshev basis of t = z^2 for conditioning and converted to
 monomial coefficients for Horner evaluation.  The script also reports the
 maximum absolute error of the float32 Horner evaluation against scipy's erf.
+
+The kernel evaluates the normal CDF directly, Phi(x) = 0.5 + x * Q(x^2) for
+|x| <= Z sqrt 2, with Q_k = P_k / (2 sqrt 2 * 2^k) (``phi_coeffs``), which
+folds the 1/sqrt 2 argument scaling and the 1/2 into the coefficients.
 
     python fuseml_amd/csrc/fit_erf.py
 """
@@ -36,6 +40,11 @@ def fit(Z=Z, D=D):
     return mono
 
 
+def phi_coeffs(mono):
+    """Coefficients of Q in Phi(x) = 0.5 + x * Q(x^2), from erf's P."""
+    return [c / (2.0 * np.sqrt(2.0) * 2.0 ** k) for k, c in enumerate(mono)]
+
+
 def max_err(mono, Z=Z):
     zt = np.linspace(0, 6, 400001).astype(np.float32)
     t32 = zt * zt
@@ -52,5 +61,6 @@ if __name__ == "__main__":
     mono = fit()
     err, at = max_err(mono)
     print(f"// erf(z) = z * P(z^2) on [0, {Z}], clamped beyond; max |error| {err:.2e} (at z={at:.3f})")
-    for k, c in enumerate(mono):
-        print(f"constexpr float kErfP{k} = {c:.9e}f;")
+    print(f"constexpr float kPhiClamp = {Z * np.sqrt(2.0):.17g}f;")
+    for k, c in enumerate(phi_coeffs(mono)):
+        print(f"constexpr float kPhiQ{k} = {c:.9e}f;")

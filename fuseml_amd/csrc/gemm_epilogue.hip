@@ -212,38 +212,36 @@ __device__ __forceinline__ void atomic_max_f32(float* p, float v) {
     atomicMin(reinterpret_cast<unsigned int*>(p), __float_as_uint(v));
 }
 
-// erf(z) ~= z * P(z^2) for |z| <= 3 and +-1 beyond: a least-squares fit of
-// erf(z)/z in z^2 (fuseml_amd/csrc/fit_erf.py), |error| <= 3.3e-5 in float32 —
-// far below 16-bit output resolution.  Only FMAs: no quarter-rate
-// transcendentals in the GELU epilogue.
-constexpr float kErfP0 = 1.128277939e+00f;
-constexpr float kErfP1 = -3.753779452e-01f;
-constexpr float kErfP2 = 1.111961758e-01f;
-constexpr float kErfP3 = -2.519724170e-02f;
-constexpr float kErfP4 = 4.275007755e-03f;
-constexpr float kErfP5 = -5.203029650e-04f;
-constexpr float kErfP6 = 4.228057854e-05f;
-constexpr float kErfP7 = -2.029208421e-06f;
-constexpr float kErfP8 = 4.312568586e-08f;
+// Standard normal CDF for GELU (approximate='none'):
+//   Phi(x) = 0.5 (1 + erf(x / sqrt 2)) ~= 0.5 + x * Q(x^2)  for |x| <= 3 sqrt 2,
+// with x clamped to that range beyond it (Phi(3 sqrt 2) = 1 - 1.1e-5).  Q is
+// the least-squares fit of erf(z)/z in z^2 on [0, 3] (fuseml_amd/csrc/fit_erf.py,
+// |erf error| <= 3.3e-5) with the 1/sqrt 2 and 1/2 scalings folded into its
+// coefficients: Q_k = P_k / (2 sqrt 2 * 2^k); |Phi error| <= 3.3e-5 in float32.
+// Only FMAs: GELU costs 12 VALU ops and no quarter-rate transcendentals.
+constexpr float kPhiClamp = 4.2426406871192851f;  // 3 sqrt 2
+constexpr float kPhiQ0 = 3.989064909e-01f;
+constexpr float kPhiQ1 = -6.635807263e-02f;
+constexpr float kPhiQ2 = 9.828446245e-03f;
+constexpr float kPhiQ3 = -1.113571280e-03f;
+constexpr float kPhiQ4 = 9.446521791e-05f;
+constexpr float kPhiQ5 = -5.748589919e-06f;
+constexpr float kPhiQ6 = 2.335694047e-07f;
+constexpr float kPhiQ7 = -5.604949355e-09f;
+constexpr float kPhiQ8 = 5.955950179e-11f;
 
-__device__ __forceinline__ float erf_poly(float z) {
-  const float zc = __builtin_amdgcn_fmed3f(z, -3.0f, 3.0f);
-  const float t = zc * zc;
-  float p = fmaf(kErfP8, t, kErfP7);
-  p = fmaf(p, t, kErfP6);
-  p = fmaf(p, t, kErfP5);
-  p = fmaf(p, t, kErfP4);
-  p = fmaf(p, t, kErfP3);
-  p = fmaf(p, t, kErfP2);
-  p = fmaf(p, t, kErfP1);
-  p = fmaf(p, t, kErfP0);
-  return __builtin_amdgcn_fmed3f(zc * p, -1.0f, 1.0f);
-}
-
-// GELU, approximate='none': x * Phi(x) = 0.5 x (1 + erf(x / sqrt 2)).
 __device__ __forceinline__ float gelu_erf(float x) {
-  const float h = 0.5f * x;
-  return fmaf(h, erf_poly(x * 0.70710678118654752f), h);
+  const float xc = __builtin_amdgcn_fmed3f(x, -kPhiClamp, kPhiClamp);
+  const float t = xc * xc;
+  float q = fmaf(kPhiQ8, t, kPhiQ7);
+  q = fmaf(q, t, kPhiQ6);
+  q = fmaf(q, t, kPhiQ5);
+  q = fmaf(q, t, kPhiQ4);
+  q = fmaf(q, t, kPhiQ3);
+  q = fmaf(q, t, kPhiQ2);
+  q = fmaf(q, t, kPhiQ1);
+  q = fmaf(q, t, kPhiQ0);
+  return x * fmaf(xc, q, 0.5f);
 }
 
 // Logistic function from the hardware exp2 and reciprocal (about 1 ulp each).
@@ -275,6 +273,11 @@ struct StageGeom {
   static_assert(kRowsPerSweep * kChunks == 16, "swizzle covers one 16-lane bank sweep");
   __device__ static __forceinline__ int swizzle(int row) { return (row / kRowsPerSweep) & (kChunks - 1); }
 };
+
+// s_waitcnt lgkmcnt(0) (LDS reads returned), other counters unconstrained.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
+}
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at maximum).
@@ -423,7 +426,7 @@ __device__ __forceinline__ void epilogue_block(KDesc& d, f32x16_t& v, int m,
 // The kernel
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int BK, int S, int WM, int WN, typename T>
+template <int BM, int BN, int BK, int S, int WM, int WN, bool PP, typename T>
 __global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   KDesc& d = *(KDesc*)(__builtin_amdgcn_kernarg_segment_ptr());
@@ -563,36 +566,111 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       });
     };
 
-    // S-stage pipeline: stages kt+1 .. kt+S-2 stay in flight while stage kt is
-    // consumed; one barrier per stage both publishes the DMA of stage kt (after
-    // each wave's own vmcnt wait) and retires the slot the next DMA overwrites.
     const int nk = (K + BK - 1) / BK;
-    static_for<0, S - 1>([&](auto p) {
-      if (p < nk) load_stage(p, p);
-    });
-    int slot = 0;
-    for (int kt = 0; kt < nk; ++kt) {
-      const int ahead = min(nk - 1 - kt, S - 2);  // stages issued after kt
-      if (ahead == S - 2) {
-        wait_vmcnt<LPS * (S - 2)>();
-      } else {
-        static_for<0, S - 2>([&](auto q) {
-          if (ahead == q) wait_vmcnt<LPS * q>();
+    if constexpr (PP) {
+      // Ping-pong: waves 0-3 and 4-7 (one of each per SIMD) alternate between a
+      // memory phase (wait for the stage's DMA, read all its fragments into
+      // registers, issue the DMA S-1 stages ahead) and a compute phase (the
+      // stage's MFMAs), one group a phase behind the other, so one group's LDS
+      // traffic runs under the other group's MFMAs.  Every wave runs 2*nk+1
+      // phases, each closed by a barrier.  Before each barrier a wave waits for
+      // its own DMAs of the stage the next memory phase reads; a memory phase
+      // also waits for its LDS reads, so the slot can be overwritten afterwards.
+      static_assert(NW == 8, "ping-pong pairs two groups of four waves");
+      const int grp = wave >> 2;
+      i32x4_t fr_a[KS][NI], fr_b[KS][NJ];
+      static_for<0, S - 1>([&](auto p) {
+        if (p < nk) load_stage(p, p);
+      });
+      int issued = min(nk, S - 1);
+      auto mem = [&](int k) {
+        const char* st = smem + (k % S) * STAGE;
+        static_for<0, KS>([&](auto ks) {
+          const int chunk = ((2 * ks + khalf) ^ swz) << 4;
+          static_for<0, NI>([&](auto i) {
+            fr_a[ks][i] = *reinterpret_cast<const i32x4_t*>(st + fa_row + 32 * i * RB + chunk);
+          });
+          static_for<0, NJ>([&](auto j) {
+            fr_b[ks][j] = *reinterpret_cast<const i32x4_t*>(st + fb_row + 32 * j * RB + chunk);
+          });
         });
+        if (k + S - 1 < nk) load_stage(k + S - 1, (k + S - 1) % S);
+        issued = min(nk, k + S);
+        wait_lgkmcnt0();
+      };
+      auto comp = [&]() {
+        static_for<0, KS>([&](auto ks) {
+          static_for<0, NI>([&](auto i) {
+            static_for<0, NJ>([&](auto j) { acc[i][j] = mfma32<T>(fr_a[ks][i], fr_b[ks][j], acc[i][j]); });
+          });
+        });
+      };
+      // End of a phase: this wave's DMAs of stage `need` (read by the next
+      // memory phase) have landed, then the workgroup barrier.
+      auto end_phase = [&](int need) {
+        if (need < nk) {
+          const int allowed = min(max(issued - need - 1, 0), S - 1);
+          static_for<0, S>([&](auto a) {
+            if (allowed == a) wait_vmcnt<LPS * a>();
+          });
+        }
+        // sched_barrier(0) keeps the scheduler from moving any instruction
+        // (MFMAs included) across the phase boundary.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      end_phase(0);    // stage 0 has landed before the first memory phase reads it
+      if (grp == 0) {  // phases 2k: mem(k), 2k+1: comp(k), 2nk: idle
+        for (int k = 0; k < nk; ++k) {
+          mem(k);
+          end_phase(k);
+          comp();
+          end_phase(k + 1);
+        }
+        end_phase(nk);
+      } else {  // phase 0: idle, 2k+1: mem(k), 2k+2: comp(k)
+        end_phase(0);
+        for (int k = 0; k < nk; ++k) {
+          mem(k);
+          end_phase(k + 1);
+          comp();
+          end_phase(k + 1);
+        }
       }
-      // A bare s_barrier: __syncthreads() would add a release fence that drains
-      // every in-flight DMA.  The asm statements only stop the compiler from
-      // moving memory accesses across the barrier.
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      if (kt + S - 1 < nk) {
-        int nslot = slot + S - 1;
-        if (nslot >= S) nslot -= S;
-        load_stage(kt + S - 1, nslot);
+    } else {
+      // S-stage pipeline: stages kt+1 .. kt+S-2 stay in flight while stage kt is
+      // consumed; one barrier per stage both publishes the DMA of stage kt (after
+      // each wave's own vmcnt wait) and retires the slot the next DMA overwrites.
+      static_for<0, S - 1>([&](auto p) {
+        if (p < nk) load_stage(p, p);
+      });
+      int slot = 0;
+      for (int kt = 0; kt < nk; ++kt) {
+        const int ahead = min(nk - 1 - kt, S - 2);  // stages issued after kt
+        if (ahead == S - 2) {
+          wait_vmcnt<LPS * (S - 2)>();
+        } else {
+          static_for<0, S - 2>([&](auto q) {
+            if (ahead == q) wait_vmcnt<LPS * q>();
+          });
+        }
+        // A bare s_barrier: __syncthreads() would add a release fence that drains
+        // every in-flight DMA.  The asm statements only stop the compiler from
+        // moving memory accesses across the barrier.
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + S - 1 < nk) {
+          int nslot = slot + S - 1;
+          if (nslot >= S) nslot -= S;
+          load_stage(kt + S - 1, nslot);
+        }
+        compute(smem + slot * STAGE);
+        if (++slot == S) slot = 0;
       }
-      compute(smem + slot * STAGE);
-      if (++slot == S) slot = 0;
     }
     __syncthreads();  // the epilogue reuses LDS
 
@@ -817,14 +895,16 @@ __global__ void reduce_fill_kernel(float* sum, float* amax, float* mean, int len
 
 struct TileConfig {
   int bm, bn, bk, stages, wm, wn;
+  bool pingpong;
   constexpr int lds_bytes() const {
     return stages * (bm + bn) * bk * 2 + kAuxSlots * (bm > bn ? bm : bn) * 4;
   }
 };
 
-constexpr TileConfig kLarge = {256, 256, 32, 4, 2, 4};  // 8 waves, 128 KB LDS, 1 workgroup/CU
-constexpr TileConfig kWide = {128, 256, 32, 3, 2, 2};   // 4 waves,  72 KB LDS, 2 workgroups/CU
-constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2};  // 4 waves,  64 KB LDS, 2 workgroups/CU
+constexpr TileConfig kLarge = {256, 256, 32, 4, 2, 4, true};   // 8 waves ping-pong, 132 KB LDS, 1 WG/CU
+constexpr TileConfig kLargeL = {256, 256, 32, 4, 2, 4, false};  // same tile, lock-step waves
+constexpr TileConfig kWide = {128, 256, 32, 3, 2, 2, false};    // 4 waves, 76 KB LDS, 2 WG/CU
+constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2, false};   // 4 waves, 66 KB LDS, 2 WG/CU
 
 constexpr int64_t kMaxBytes = (int64_t)1 << 31;
 
@@ -834,6 +914,7 @@ TileConfig choose_config(const fuseml_gemm_desc& d) {
   // FUSEML_HIP_TILE=large|wide|small pins a variant (tuning sweeps).
   if (const char* force = getenv("FUSEML_HIP_TILE")) {
     if (!strcmp(force, "large")) return kLarge;
+    if (!strcmp(force, "lockstep")) return kLargeL;
     if (!strcmp(force, "wide")) return kWide;
     if (!strcmp(force, "small")) return kSmall;
   }
@@ -998,10 +1079,10 @@ hipError_t launch_variant(const fuseml_gemm_desc& d, hipStream_t stream) {
   const int64_t tiles = cdiv(d.M, C.bm) * cdiv(d.N, C.bn);
   const dim3 grid((unsigned)tiles), block(C.wm * C.wn * 64);
   if (d.ab_dtype == FUSEML_BF16)
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, __bf16>), grid,
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.pingpong, __bf16>), grid,
                        block, 0, stream, d);
   else
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, _Float16>), grid,
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.pingpong, _Float16>), grid,
                        block, 0, stream, d);
   return hipGetLastError();
 }
@@ -1084,8 +1165,10 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
   }
 
   const TileConfig c = choose_config(d);
-  if (c.bm == kLarge.bm && c.bn == kLarge.bn)
+  if (c.bm == kLarge.bm && c.bn == kLarge.bn && c.pingpong)
     e = launch_variant<kLarge>(d, stream);
+  else if (c.bm == kLargeL.bm && c.bn == kLargeL.bn)
+    e = launch_variant<kLargeL>(d, stream);
   else if (c.bm == kWide.bm && c.bn == kWide.bn)
     e = launch_variant<kWide>(d, stream);
   else

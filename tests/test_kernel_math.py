@@ -1,9 +1,9 @@
 """Host-side checks of the kernels' closed-form math.
 
-The erf polynomial constants are read from the HIP source and evaluated in
-float32 exactly as the kernel's Horner scheme does, then compared with
-scipy's erf (the library routine) and with the closed-form GELU identities.
-The fit itself is reproduced from fuseml_amd/csrc/fit_erf.py.
+The GELU constants (the normal-CDF polynomial) are read from the HIP source
+and evaluated in float32 exactly as the kernel's Horner scheme does, then
+compared with scipy's erf (the library routine), with the closed-form GELU and
+its identities, and with the fit script that produced them.
 """
 
 import math
@@ -18,45 +18,51 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SRC = os.path.join(REPO, "fuseml_amd", "csrc", "gemm_epilogue.hip")
 
 
-def _coeffs():
+def _consts():
     text = open(SRC).read()
-    found = dict(re.findall(r"constexpr float kErfP(\d) = ([-+0-9.eE]+)f;", text))
-    return [np.float32(float(found[str(k)])) for k in range(len(found))]
+    q = dict(re.findall(r"constexpr float kPhiQ(\d) = ([-+0-9.eE]+)f;", text))
+    clamp = float(re.search(r"constexpr float kPhiClamp = ([-+0-9.eE]+)f;", text).group(1))
+    return [np.float32(float(q[str(k)])) for k in range(len(q))], np.float32(clamp)
 
 
-def erf_poly32(z):
-    c = _coeffs()
-    z = np.asarray(z, dtype=np.float32)
-    zc = np.clip(z, np.float32(-3.0), np.float32(3.0))
-    t = zc * zc
-    p = c[-1]
-    for ck in c[-2::-1]:
-        p = p * t + ck  # the kernel uses fma; float32 rounding differs by < 1 ulp
-    return np.clip(zc * p, np.float32(-1.0), np.float32(1.0))
+def phi32(x):
+    """The kernel's Phi(x) = 0.5 + xc * Q(xc^2), xc = clamp(x), in float32."""
+    q, c = _consts()
+    x = np.asarray(x, dtype=np.float32)
+    xc = np.clip(x, -c, c)
+    t = xc * xc
+    p = q[-1]
+    for qk in q[-2::-1]:
+        p = p * t + qk  # the kernel uses fma; float32 rounding differs by < 1 ulp
+    return xc * p + np.float32(0.5)
 
 
-def test_erf_polynomial_error_bound():
-    z = np.linspace(-8, 8, 400001, dtype=np.float32)
-    err = np.abs(erf_poly32(z).astype(np.float64) - erf(z.astype(np.float64)))
-    assert err.max() < 4e-5, err.max()
+def gelu32(x):
+    x = np.asarray(x, dtype=np.float32)
+    return x * phi32(x)
 
 
-def test_erf_polynomial_is_odd_and_saturates():
-    z = np.linspace(0, 8, 10001, dtype=np.float32)
-    assert np.array_equal(erf_poly32(-z), -erf_poly32(z))
-    assert erf_poly32(np.float32(0.0)) == 0.0
-    assert np.all(np.abs(erf_poly32(np.float32([3.5, 6.0, 1e30]))) == 1.0)
+def test_phi_error_bound():
+    x = np.linspace(-12, 12, 600001, dtype=np.float32)
+    ref = 0.5 * (1 + erf(x.astype(np.float64) / math.sqrt(2)))
+    assert np.abs(phi32(x) - ref).max() < 4e-5
 
 
-def test_gelu_from_poly_matches_closed_form():
-    x = np.linspace(-8, 8, 200001, dtype=np.float32)
-    h = np.float32(0.5) * x
-    g = h * erf_poly32(x * np.float32(1 / math.sqrt(2))) + h
+def test_phi_symmetry_and_range():
+    x = np.linspace(0, 12, 10001, dtype=np.float32)
+    assert np.allclose(phi32(x) + phi32(-x), 1.0, atol=1e-6)       # Phi(x) + Phi(-x) = 1
+    assert phi32(np.float32(0.0)) == np.float32(0.5)
+    assert np.all((phi32(x) > 0.49) & (phi32(x) < 1.0 + 5e-5))
+
+
+def test_gelu_matches_closed_form():
+    x = np.linspace(-10, 10, 200001, dtype=np.float32)
     ref = 0.5 * x.astype(np.float64) * (1 + erf(x.astype(np.float64) / math.sqrt(2)))
-    assert np.abs(g - ref).max() < 2e-4
-    # GELU(x) - GELU(-x) = x holds for the exact function and for the odd erf approximation
-    gm = (np.float32(-0.5) * x) * erf_poly32(-x * np.float32(1 / math.sqrt(2))) + np.float32(-0.5) * x
-    assert np.allclose(g - gm, x, atol=1e-5)
+    err = np.abs(gelu32(x) - ref)
+    assert err.max() < 2e-4                       # absolute, over |x| <= 10
+    big = np.abs(x) > 0.5
+    assert (err[big] / np.abs(ref[big] + 1e-30)).max() < 1e-3 or err[big].max() < 2e-4
+    assert np.allclose(gelu32(x) - gelu32(-x), x, atol=2e-5)   # GELU(x) - GELU(-x) = x
 
 
 def test_fit_script_reproduces_constants():
@@ -64,7 +70,9 @@ def test_fit_script_reproduces_constants():
     import fit_erf
 
     mono = fit_erf.fit()
-    assert np.allclose(np.float32(mono), np.array(_coeffs()), rtol=1e-6, atol=1e-12)
+    q, clamp = _consts()
+    assert np.allclose(np.float32(fit_erf.phi_coeffs(mono)), np.array(q), rtol=1e-6, atol=1e-14)
+    assert math.isclose(float(clamp), fit_erf.Z * math.sqrt(2), rel_tol=1e-7)
     err, _ = fit_erf.max_err(mono)
     assert err < 4e-5
 
