@@ -287,6 +287,39 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Epilogue code prefetch.  Every launch starts with cold instruction caches,
+// and the epilogue runs once per tile after the K loop, so its first execution
+// on a CU takes one instruction-cache miss per 64-byte line in sequence.  The
+// K loop pulls the epilogue's machine code into L2 with ordinary vector loads
+// shortly before it ends, so those misses are served by L2.  The byte range is
+// the epilogue's own code, [label 7, label 8) of this function, computed by the
+// assembler relative to s_getpc_b64 (which returns the address of the next
+// instruction, the s_mov).
+struct CodeSpan {
+  uint64_t pc;   // address of the s_mov after s_getpc
+  int32_t off;   // epilogue start - pc
+  int32_t len;   // epilogue bytes
+};
+
+__device__ __forceinline__ CodeSpan epilogue_code_span() {
+  CodeSpan c;
+  asm volatile("s_getpc_b64 %0\n\ts_mov_b32 %1, 7f-.\n\ts_mov_b32 %2, 8f-7f"
+               : "=s"(c.pc), "=s"(c.off), "=s"(c.len));
+  return c;
+}
+
+// One dword from each of 64 consecutive 64-byte lines of part `part` of the
+// span.  The buffer's size is the span, so loads past its end return zero.  The
+// destination register must stay live until a vmcnt(0) wait: the load is not
+// visible to the compiler's wait-count tracking (which can then only over-wait).
+__device__ __forceinline__ void prefetch_code(const CodeSpan& c, int part, int lane, uint32_t& junk) {
+  if (c.off <= 0 || c.len <= 0 || c.len >= (1 << 22)) return;
+  const __amdgpu_buffer_rsrc_t r =
+      make_rsrc(reinterpret_cast<const void*>(c.pc + (uint64_t)c.off), (uint32_t)c.len);
+  const uint32_t voff = (uint32_t)(part * 64 + lane) * 64u;
+  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(junk) : "v"(voff), "s"(r) : "memory");
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
 // wherever an accumulator array is indexed, so every index is a constant and
 // the arrays stay in registers whatever the unroller decides.
@@ -315,119 +348,15 @@ __device__ __forceinline__ int stage_chunk(int r, int c) {  // 16-byte chunk c o
 
 __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, x.w, x.x, x.y}; }
 
-// Run the epilogue op chain on one 32x32 accumulator block of this lane:
-// v[4g+e] is element (m, nb + 8g + e), and (r_loc, u0 + 2g) its staging row
-// and unit.  Operand `staged` (if >= 0) is read from the LDS staging tile
-// instead of global memory.  The chain is read from the kernel arguments, so
-// the loop and its switch are uniform (scalar) control flow.
-template <int BN, int AUXLEN>
-__device__ __forceinline__ void epilogue_block(KDesc& d, f32x16_t& v, int m,
-                                               int nb, int M, int N, int staged,
-                                               const char* stg, int r_loc, int u0,
-                                               const float* aux, int m_loc, int n_loc) {
-  for (int o = 0; o < d.n_ops; ++o) {
-    const int kind = d.ops[o].kind;
-    const float sc = d.ops[o].scalar;
-    const int oi = d.ops[o].operand;
-    switch (kind) {
-      case FUSEML_OP_ADD:
-      case FUSEML_OP_MUL: {
-        float x[16];
-        const int fl = d.operands[oi].reserved;
-        if (fl & kFlagAux) {
-          const float* a = aux + ((fl >> 8) & (kAuxSlots - 1)) * AUXLEN;
-          if (d.operands[oi].stride_m == 0) {  // row vector: four runs of 4 columns
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const float4 q = *reinterpret_cast<const float4*>(a + n_loc + 8 * g);
-              x[4 * g + 0] = q.x;
-              x[4 * g + 1] = q.y;
-              x[4 * g + 2] = q.z;
-              x[4 * g + 3] = q.w;
-            }
-          } else {  // column vector: one value per row
-            const float q = a[m_loc];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) x[r] = q;
-          }
-        } else if (oi == staged) {
-          const int dt = d.operands[oi].dtype;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const uint2 w = *reinterpret_cast<const uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g));
-            x[4 * g + 0] = elem_to_f32(w.x & 0xffffu, dt);
-            x[4 * g + 1] = elem_to_f32(w.x >> 16, dt);
-            x[4 * g + 2] = elem_to_f32(w.y & 0xffffu, dt);
-            x[4 * g + 3] = elem_to_f32(w.y >> 16, dt);
-          }
-        } else {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int n = nb + 8 * g;
-            load_operand4(d.operands[oi], m, n, m < M && n < N, x + 4 * g);
-          }
-        }
-        if (kind == FUSEML_OP_ADD) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) v[r] = fmaf(sc, x[r], v[r]);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) v[r] = v[r] * x[r];
-        }
-        break;
-      }
-      case FUSEML_OP_STORE: {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float x[4] = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
-          store_out4(d.extra[oi], m, nb + 8 * g, M, N, x);
-        }
-        break;
-      }
-      case FUSEML_OP_RELU:
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
-        break;
-      case FUSEML_OP_GELU_ERF:
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = gelu_erf(v[r]);
-        break;
-      case FUSEML_OP_GELU_TANH:
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = gelu_tanh(v[r]);
-        break;
-      case FUSEML_OP_SIGMOID:
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = sigmoid(v[r]);
-        break;
-      case FUSEML_OP_SCALE:
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = v[r] * sc;
-        break;
-      case FUSEML_OP_ADD_SCALAR:
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = v[r] + sc;
-        break;
-      case FUSEML_OP_ADD_SELF:
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = fmaf(sc, v[r], v[r]);
-        break;
-      case FUSEML_OP_MUL_SELF:
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = v[r] * v[r];
-        break;
-      default:
-        break;
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int BK, int S, int WM, int WN, bool PP, typename T>
-__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(2)))
+// SCHED selects the K-loop schedule: 0 lock-step waves, 1 ping-pong (8 waves,
+// two per SIMD), 2 one wave per SIMD with the barrier between the stage's two
+// MFMA k-steps (4 waves, 128x128 wave tiles, accumulators in AGPRs).
+template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T>
+__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED == 2 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   KDesc& d = *(KDesc*)(__builtin_amdgcn_kernarg_segment_ptr());
   using G = StageGeom<BK>;
@@ -455,6 +384,12 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const CodeSpan code = epilogue_code_span();
+  uint32_t code_junk = 0;
+  // Code prefetch part of this wave: the workgroups an XCD runs together (the
+  // hardware deals them round-robin over the 8 XCDs) split the span between
+  // their first four waves, 64 lines each.
+  const int code_part = ((blockIdx.x >> 3) & 31) * 4 + (wave & 3);
   const int wm = wave / WN;
   const int wn = wave % WN;
 
@@ -484,6 +419,30 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     const uint32_t b_bytes = (uint32_t)(((int64_t)(N - 1) * d.ldb + K) * 2);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(d.a, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(d.b, b_bytes);
+
+    // Vector operands with an LDS slot (bias and the like): this thread's element
+    // of each is loaded now, lands during the K loop, and is written to its slot
+    // (as fp32) after it.  Every slot holds at most one element per thread.
+    static_assert(AUXLEN <= NT, "one staged vector element per thread");
+    uint32_t aux_bits[kAuxSlots];
+    static_for<0, kAuxSlots>([&](auto q) { aux_bits[q] = 0; });
+    for (int oi = 0; oi < d.n_operands; ++oi) {
+      const int fl = d.operands[oi].reserved;
+      if (!(fl & kFlagAux)) continue;
+      const bool rowv = d.operands[oi].stride_m == 0;
+      const int idx = (rowv ? n0 : m0) + tid;
+      const bool ok = tid < (rowv ? BN : BM) && idx < (rowv ? N : M);
+      const int64_t st = rowv ? d.operands[oi].stride_n : d.operands[oi].stride_m;
+      const int eb = d.operands[oi].dtype == FUSEML_F32 ? 4 : 2;
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(d.operands[oi].ptr, (uint32_t)(d.operands[oi].extent * eb));
+      const uint32_t off = ok ? (uint32_t)((int64_t)idx * st * eb) : kOOB;
+      const uint32_t bits = (eb == 4) ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)
+                                      : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+      const int slot = (fl >> 8) & (kAuxSlots - 1);
+      static_for<0, kAuxSlots>([&](auto q) {
+        if (slot == q) aux_bits[q] = bits;
+      });
+    }
 
     // Global -> LDS DMA.  One wave-wide buffer_load_dwordx4 ... lds writes 64 x 16
     // bytes contiguously from the LDS base in M0, i.e. kRowsPerDma whole stage
@@ -567,7 +526,80 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     };
 
     const int nk = (K + BK - 1) / BK;
-    if constexpr (PP) {
+    // Workgroup barrier that keeps the compiler from moving any instruction
+    // (MFMAs included) across it.  A bare s_barrier: __syncthreads() would add a
+    // release fence that drains every in-flight DMA.
+    auto barrier = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    if constexpr (SCHED == 2) {
+      // One wave per SIMD.  Stage k is consumed in two MFMA k-steps:
+      //   (1) k-step 0's MFMAs run while k-step 1's fragments are read and the
+      //       DMA of stage k+S-1 is issued (into the slot of stage k-1);
+      //   (2) this wave's LDS reads of stage k are complete and its DMAs of
+      //       stage k+1 have landed; then the workgroup barrier, after which
+      //       stage k+1 is visible to every wave;
+      //   (3) k-step 1's MFMAs (fragments already in registers) run while stage
+      //       k+1's k-step 0 fragments are read.
+      // The MFMA pipe drains only for the barrier itself.  A DMA issued in
+      // iteration k overwrites the slot of stage k-1, whose last reads every
+      // wave completed before the barrier of iteration k-1.
+      static_assert(KS == 2, "two MFMA k-steps per stage");
+      i32x4_t f0a[NI], f0b[NJ], f1a[NI], f1b[NJ];
+      auto read = [&](const char* st, int ks, i32x4_t* fa, i32x4_t* fb) {
+        const int chunk = ((2 * ks + khalf) ^ swz) << 4;
+        static_for<0, NI>([&](auto i) {
+          fa[i] = *reinterpret_cast<const i32x4_t*>(st + fa_row + 32 * i * RB + chunk);
+        });
+        static_for<0, NJ>([&](auto j) {
+          fb[j] = *reinterpret_cast<const i32x4_t*>(st + fb_row + 32 * j * RB + chunk);
+        });
+      };
+      auto mma = [&](const i32x4_t* fa, const i32x4_t* fb) {
+        static_for<0, NI>([&](auto i) {
+          static_for<0, NJ>([&](auto j) { acc[i][j] = mfma32<T>(fa[i], fb[j], acc[i][j]); });
+        });
+      };
+      static_for<0, S - 1>([&](auto p) {
+        if (p < nk) load_stage(p, p);
+      });
+      int issued = min(nk, S - 1);
+      // This wave's DMAs of stage `need` have landed (the later stages may stay in flight).
+      auto wait_stage = [&](int need) {
+        if (need >= nk) return;
+        const int allowed = min(max(issued - need - 1, 0), S - 2);
+        static_for<0, S - 1>([&](auto a) {
+          if (allowed == a) wait_vmcnt<LPS * a>();
+        });
+      };
+      wait_stage(0);
+      barrier();
+      read(smem, 0, f0a, f0b);
+      int slot = 0;
+      for (int k = 0; k < nk; ++k) {
+        const char* st = smem + slot * STAGE;
+        if (++slot == S) slot = 0;
+        // Every DMA has landed at the start of the last iteration.
+        if (k == nk - 1) prefetch_code(code, code_part, lane, code_junk);
+        read(st, 1, f1a, f1b);
+        if (k + S - 1 < nk) {
+          int ls = slot + S - 2;
+          if (ls >= S) ls -= S;
+          load_stage(k + S - 1, ls);
+        }
+        issued = min(nk, k + S);
+        mma(f0a, f0b);
+        wait_lgkmcnt0();
+        wait_stage(k + 1);
+        barrier();
+        if (k + 1 < nk) read(smem + slot * STAGE, 0, f0a, f0b);
+        mma(f1a, f1b);
+      }
+    } else if constexpr (SCHED == 1) {
       // Ping-pong: waves 0-3 and 4-7 (one of each per SIMD) alternate between a
       // memory phase (wait for the stage's DMA, read all its fragments into
       // registers, issue the DMA S-1 stages ahead) and a compute phase (the
@@ -576,7 +608,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       // phases, each closed by a barrier.  Before each barrier a wave waits for
       // its own DMAs of the stage the next memory phase reads; a memory phase
       // also waits for its LDS reads, so the slot can be overwritten afterwards.
-      static_assert(NW == 8, "ping-pong pairs two groups of four waves");
+      static_assert(NW == 8 && KS == 2, "ping-pong pairs two groups of four waves");
       const int grp = wave >> 2;
       i32x4_t fr_a[KS][NI], fr_b[KS][NJ];
       static_for<0, S - 1>([&](auto p) {
@@ -607,11 +639,19 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       };
       // End of a phase: this wave's DMAs of stage `need` (read by the next
       // memory phase) have landed, then the workgroup barrier.
+      // A code prefetch issued after the last DMA (pf = 1) is the newest vector
+      // memory op: one more op may stay outstanding.
+      int pf = 0;
       auto end_phase = [&](int need) {
         if (need < nk) {
           const int allowed = min(max(issued - need - 1, 0), S - 1);
           static_for<0, S>([&](auto a) {
-            if (allowed == a) wait_vmcnt<LPS * a>();
+            if (allowed == a) {
+              if (pf)
+                wait_vmcnt<LPS * a + 1>();
+              else
+                wait_vmcnt<LPS * a>();
+            }
           });
         }
         // sched_barrier(0) keeps the scheduler from moving any instruction
@@ -627,6 +667,12 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         for (int k = 0; k < nk; ++k) {
           mem(k);
           end_phase(k);
+          // Two stages before the end, every DMA has been issued: the prefetch
+          // has a stage of MFMAs to land in before the epilogue.
+          if (k == max(nk - 2, 0)) {
+            prefetch_code(code, code_part, lane, code_junk);
+            pf = 1;
+          }
           comp();
           end_phase(k + 1);
         }
@@ -668,11 +714,26 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           if (nslot >= S) nslot -= S;
           load_stage(kt + S - 1, nslot);
         }
+        // Every DMA has landed at the start of the last iteration.
+        if (kt == nk - 1) prefetch_code(code, code_part, lane, code_junk);
         compute(smem + slot * STAGE);
         if (++slot == S) slot = 0;
       }
     }
-    __syncthreads();  // the epilogue reuses LDS
+    asm volatile("7:");  // start of the prefetched epilogue code
+    for (int oi = 0; oi < d.n_operands; ++oi) {
+      const int fl = d.operands[oi].reserved;
+      if (!(fl & kFlagAux) || tid >= (d.operands[oi].stride_m == 0 ? BN : BM)) continue;
+      const int slot = (fl >> 8) & (kAuxSlots - 1);
+      const int dt = d.operands[oi].dtype;
+      static_for<0, kAuxSlots>([&](auto q) {
+        if (slot == q) aux[q * AUXLEN + tid] = elem_to_f32(aux_bits[q], dt);
+      });
+    }
+    __syncthreads();  // the epilogue reuses the stage LDS; the vector slots are written
+    // The barrier's release fence waited for every vector memory op (vmcnt(0)),
+    // the code prefetch included: its register is free from here on.
+    asm volatile("" ::"v"(code_junk));
 
     // ---------------------------------------------------------------------
     // Epilogue.  In accumulator block (i,j), register r of this lane holds
@@ -696,31 +757,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     const int crow = tid / CPR;  // cooperative-pass row and chunk of this thread
     const int cchk = tid % CPR;
 
-    // (1) Stage the epilogue operands in LDS: every vector operand the host gave
-    // an aux slot (as fp32), and the first LDS-eligible 2-D operand of the chain.
-    // All global loads of this phase are in flight together; one barrier.
-    bool any_aux = false;
-    for (int oi = 0; oi < d.n_operands; ++oi) {
-      const int fl = d.operands[oi].reserved;
-      if (!(fl & kFlagAux)) continue;
-      any_aux = true;
-      float* a = aux + ((fl >> 8) & (kAuxSlots - 1)) * AUXLEN;
-      const bool rowv = d.operands[oi].stride_m == 0;
-      const int len = rowv ? BN : BM;
-      const int base = rowv ? n0 : m0;
-      const int lim = rowv ? N : M;
-      const int64_t st = rowv ? d.operands[oi].stride_n : d.operands[oi].stride_m;
-      const int dt = d.operands[oi].dtype;
-      const int eb = dt == FUSEML_F32 ? 4 : 2;
-      const __amdgpu_buffer_rsrc_t r = make_rsrc(d.operands[oi].ptr, (uint32_t)(d.operands[oi].extent * eb));
-      for (int t = tid; t < len; t += NT) {
-        const int idx = base + t;
-        const uint32_t off = idx < lim ? (uint32_t)((int64_t)idx * st * eb) : kOOB;
-        const uint32_t bits = (eb == 4) ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)
-                                        : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-        a[t] = elem_to_f32(bits, dt);
-      }
-    }
+    // (1) Stage the epilogue operands in LDS: the first LDS-eligible 2-D operand
+    // of the chain (all its global loads in flight together, one barrier).  The
+    // vector operands were written to their slots before the barrier above.
     int staged = -1;
     for (int o = 0; o < d.n_ops; ++o) {
       const int k = d.ops[o].kind;
@@ -742,15 +781,142 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         *reinterpret_cast<i32x4_t*>(stg + stage_chunk<BN>(rl, cchk)) = x;
       });
     }
-    if (staged >= 0 || any_aux) __syncthreads();
+    if (staged >= 0) __syncthreads();
 
-    // (2) Op chain on every block, in registers; reduction partials.
+    // (2) The op chain, one column block at a time: for column block i, each op
+    // runs over the NJ row blocks (NJ*16 independent elements) before the next
+    // op, so each op's descriptor is read NI times rather than NI*NJ, and a row
+    // vector's values (which depend only on the column) are read from LDS once
+    // per column block.  Carrying one column block (not all of them) through the
+    // runtime op loop keeps the loop's live values within the register file.
+    const bool use_stage_out = d.out.ptr != nullptr && (d.out.reserved & kFlagStage) && !col_red;
+    static_for<0, NI>([&](auto i) {
+      for (int o = 0; o < d.n_ops; ++o) {
+        // Lane coordinates through an opaque copy: the per-block addresses derived
+        // from them are recomputed inside each op instead of being hoisted out of
+        // the loop and held.
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int l32 = ln & 31;
+        const int khalf = ln >> 5;
+        const int mw = m0 + wm * TM + l32;
+        const int nb = n0 + wn * TN + 32 * i + 4 * khalf;  // first column of block i
+        const int kind = d.ops[o].kind;
+        const float sc = d.ops[o].scalar;
+        const int oi = d.ops[o].operand;
+        if (kind == FUSEML_OP_ADD || kind == FUSEML_OP_MUL) {
+          const int fl = d.operands[oi].reserved;
+          const bool is_add = kind == FUSEML_OP_ADD;
+          // v <- v + sc*x (ADD) or v * x (MUL), over one block's 16 elements.
+          auto combine = [&](f32x16_t& v, const float* x) {
+            if (is_add) {
+              static_for<0, 16>([&](auto r) { v[(int)r] = fmaf(sc, x[r], v[(int)r]); });
+            } else {
+              static_for<0, 16>([&](auto r) { v[(int)r] = v[(int)r] * x[r]; });
+            }
+          };
+          if (fl & kFlagAux) {
+            const float* av = aux + ((fl >> 8) & (kAuxSlots - 1)) * AUXLEN;
+            if (d.operands[oi].stride_m == 0) {  // row vector: four runs of 4 columns
+              float x[16];
+              static_for<0, 4>([&](auto g) {
+                const float4 q = *reinterpret_cast<const float4*>(av + (nb - n0) + 8 * g);
+                x[4 * g + 0] = q.x;
+                x[4 * g + 1] = q.y;
+                x[4 * g + 2] = q.z;
+                x[4 * g + 3] = q.w;
+              });
+              static_for<0, NJ>([&](auto j) { combine(acc[i][j], x); });
+            } else {  // column vector: one value per row
+              static_for<0, NJ>([&](auto j) {
+                const float q = av[wm * TM + 32 * j + l32];
+                float x[16];
+                static_for<0, 16>([&](auto r) { x[r] = q; });
+                combine(acc[i][j], x);
+              });
+            }
+          } else if (oi == staged) {
+            const int dt = d.operands[oi].dtype;
+            const int u0 = (wn * TN + 32 * i) / 4 + khalf;
+            static_for<0, NJ>([&](auto j) {
+              const int r_loc = wm * TM + 32 * j + l32;
+              float x[16];
+              static_for<0, 4>([&](auto g) {
+                const uint2 w = *reinterpret_cast<const uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g));
+                x[4 * g + 0] = elem_to_f32(w.x & 0xffffu, dt);
+                x[4 * g + 1] = elem_to_f32(w.x >> 16, dt);
+                x[4 * g + 2] = elem_to_f32(w.y & 0xffffu, dt);
+                x[4 * g + 3] = elem_to_f32(w.y >> 16, dt);
+              });
+              combine(acc[i][j], x);
+            });
+          } else {
+            static_for<0, NJ>([&](auto j) {
+              const int m = mw + 32 * j;
+              float x[16];
+              static_for<0, 4>([&](auto g) {
+                const int n = nb + 8 * g;
+                load_operand4(d.operands[oi], m, n, m < M && n < N, x + 4 * g);
+              });
+              combine(acc[i][j], x);
+            });
+          }
+          continue;
+        }
+        switch (kind) {
+          case FUSEML_OP_STORE:
+            static_for<0, NJ>([&](auto j) {
+              static_for<0, 4>([&](auto g) {
+                const float x[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                    acc[i][j][4 * g + 3]};
+                store_out4(d.extra[oi], mw + 32 * j, nb + 8 * g, M, N, x);
+              });
+            });
+            break;
+#define FUSEML_EACH(expr)                                \
+  static_for<0, NJ>([&](auto j) {                        \
+    static_for<0, 16>([&](auto r) {                      \
+      const float v = acc[i][j][(int)r];                 \
+      acc[i][j][(int)r] = (expr);                        \
+    });                                                  \
+  })
+          case FUSEML_OP_RELU:
+            FUSEML_EACH(v > 0.0f ? v : 0.0f);
+            break;
+          case FUSEML_OP_GELU_ERF:
+            FUSEML_EACH(gelu_erf(v));
+            break;
+          case FUSEML_OP_GELU_TANH:
+            FUSEML_EACH(gelu_tanh(v));
+            break;
+          case FUSEML_OP_SIGMOID:
+            FUSEML_EACH(sigmoid(v));
+            break;
+          case FUSEML_OP_SCALE:
+            FUSEML_EACH(v * sc);
+            break;
+          case FUSEML_OP_ADD_SCALAR:
+            FUSEML_EACH(v + sc);
+            break;
+          case FUSEML_OP_ADD_SELF:
+            FUSEML_EACH(fmaf(sc, v, v));
+            break;
+          case FUSEML_OP_MUL_SELF:
+            FUSEML_EACH(v * v);
+            break;
+#undef FUSEML_EACH
+          default:
+            break;
+        }
+      }
+    });
+
+    // Unstaged output stores and reduction partials over the final values.
     float rs[NJ], rmx[NJ];
     static_for<0, NJ>([&](auto j) {
       rs[j] = 0.0f;
       rmx[j] = -INFINITY;
     });
-    const bool use_stage_out = d.out.ptr != nullptr && (d.out.reserved & kFlagStage) && !col_red;
     float* red_sum = reinterpret_cast<float*>(smem);
     float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
 
@@ -763,10 +929,6 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       static_for<0, NJ>([&](auto j) {
         const int m = mw + 32 * j;
         const int nb = nw + 32 * i;
-        const int r_loc = wm * TM + 32 * j + l32;
-        const int u0 = (wn * TN + 32 * i) / 4 + khalf;
-        epilogue_block<BN, AUXLEN>(d, acc[i][j], m, nb, M, N, staged, stg, r_loc, u0, aux,
-                                   r_loc, nb - n0);
         if (d.out.ptr != nullptr && !use_stage_out) {
           static_for<0, 4>([&](auto g) {
             const float x[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
@@ -831,7 +993,10 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         });
       });
       __syncthreads();
-      static_for<0, BM / RPP>([&](auto p) {
+      // A short loop rather than BM/RPP unrolled passes: this code runs once per
+      // tile, and its size is paid in instruction-cache misses.
+#pragma unroll 4
+      for (int p = 0; p < BM / RPP; ++p) {
         const int rl = p * RPP + crow;
         const int m = m0 + rl, n = n0 + 8 * cchk;
         i32x4_t x = *reinterpret_cast<const i32x4_t*>(stg + stage_chunk<BN>(rl, cchk));
@@ -840,9 +1005,10 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           uint16_t* dst = reinterpret_cast<uint16_t*>(d.out.ptr) + (int64_t)m * d.out.ld + n;
           *reinterpret_cast<i32x4_t*>(dst) = x;
         }
-      });
+      }
     }
 
+    asm volatile("8:");  // end of the prefetched epilogue code
     if (d.reduce_mask == 0) return;
     if (row_red) {
       if (use_stage_out) __syncthreads();  // LDS staging tile is being drained
@@ -895,24 +1061,26 @@ __global__ void reduce_fill_kernel(float* sum, float* amax, float* mean, int len
 
 struct TileConfig {
   int bm, bn, bk, stages, wm, wn;
-  bool pingpong;
+  int sched;  // K-loop schedule (kernel template parameter SCHED)
   constexpr int lds_bytes() const {
     return stages * (bm + bn) * bk * 2 + kAuxSlots * (bm > bn ? bm : bn) * 4;
   }
 };
 
-constexpr TileConfig kLarge = {256, 256, 32, 4, 2, 4, true};   // 8 waves ping-pong, 132 KB LDS, 1 WG/CU
-constexpr TileConfig kLargeL = {256, 256, 32, 4, 2, 4, false};  // same tile, lock-step waves
-constexpr TileConfig kWide = {128, 256, 32, 3, 2, 2, false};    // 4 waves, 76 KB LDS, 2 WG/CU
-constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2, false};   // 4 waves, 66 KB LDS, 2 WG/CU
+constexpr TileConfig kQuad = {256, 256, 32, 4, 2, 2, 2};   // 4 waves (1/SIMD), 128x128 wave tiles, 132 KB LDS
+constexpr TileConfig kLarge = {256, 256, 32, 4, 2, 4, 1};  // 8 waves ping-pong, 132 KB LDS, 1 WG/CU
+constexpr TileConfig kLargeL = {256, 256, 32, 4, 2, 4, 0}; // same tile, lock-step waves
+constexpr TileConfig kWide = {128, 256, 32, 3, 2, 2, 0};   // 4 waves, 76 KB LDS, 2 WG/CU
+constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2, 0};  // 4 waves, 66 KB LDS, 2 WG/CU
 
 constexpr int64_t kMaxBytes = (int64_t)1 << 31;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 TileConfig choose_config(const fuseml_gemm_desc& d) {
-  // FUSEML_HIP_TILE=large|wide|small pins a variant (tuning sweeps).
+  // FUSEML_HIP_TILE=quad|large|lockstep|wide|small pins a variant (tuning sweeps).
   if (const char* force = getenv("FUSEML_HIP_TILE")) {
+    if (!strcmp(force, "quad")) return kQuad;
     if (!strcmp(force, "large")) return kLarge;
     if (!strcmp(force, "lockstep")) return kLargeL;
     if (!strcmp(force, "wide")) return kWide;
@@ -1079,10 +1247,10 @@ hipError_t launch_variant(const fuseml_gemm_desc& d, hipStream_t stream) {
   const int64_t tiles = cdiv(d.M, C.bm) * cdiv(d.N, C.bn);
   const dim3 grid((unsigned)tiles), block(C.wm * C.wn * 64);
   if (d.ab_dtype == FUSEML_BF16)
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.pingpong, __bf16>), grid,
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16>), grid,
                        block, 0, stream, d);
   else
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.pingpong, _Float16>), grid,
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, _Float16>), grid,
                        block, 0, stream, d);
   return hipGetLastError();
 }
@@ -1165,7 +1333,9 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
   }
 
   const TileConfig c = choose_config(d);
-  if (c.bm == kLarge.bm && c.bn == kLarge.bn && c.pingpong)
+  if (c.bm == kQuad.bm && c.bn == kQuad.bn && c.sched == kQuad.sched)
+    e = launch_variant<kQuad>(d, stream);
+  else if (c.bm == kLarge.bm && c.bn == kLarge.bn && c.sched == kLarge.sched)
     e = launch_variant<kLarge>(d, stream);
   else if (c.bm == kLargeL.bm && c.bn == kLargeL.bn)
     e = launch_variant<kLargeL>(d, stream);
