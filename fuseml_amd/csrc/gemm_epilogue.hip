@@ -230,34 +230,6 @@ constexpr float kPhiQ6 = 2.335694047e-07f;
 constexpr float kPhiQ7 = -5.604949355e-09f;
 constexpr float kPhiQ8 = 5.955950179e-11f;
 
-__device__ __forceinline__ float gelu_erf(float x) {
-  const float xc = __builtin_amdgcn_fmed3f(x, -kPhiClamp, kPhiClamp);
-  const float t = xc * xc;
-  float q = fmaf(kPhiQ8, t, kPhiQ7);
-  q = fmaf(q, t, kPhiQ6);
-  q = fmaf(q, t, kPhiQ5);
-  q = fmaf(q, t, kPhiQ4);
-  q = fmaf(q, t, kPhiQ3);
-  q = fmaf(q, t, kPhiQ2);
-  q = fmaf(q, t, kPhiQ1);
-  q = fmaf(q, t, kPhiQ0);
-  return x * fmaf(xc, q, 0.5f);
-}
-
-// Logistic function from the hardware exp2 and reciprocal (about 1 ulp each).
-__device__ __forceinline__ float sigmoid(float x) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
-}
-
-// GELU, approximate='tanh': 0.5 x (1 + tanh(u)) with u = sqrt(2/pi)(x + 0.044715 x^3)
-// (Hendrycks & Gimpel 2016).  Since 0.5 (1 + tanh(u)) = sigmoid(2u), this is
-// x * sigmoid(2u).
-__device__ __forceinline__ float gelu_tanh(float x) {
-  constexpr float kC = 0.79788456080286536f;  // sqrt(2/pi)
-  const float two_u = 2.0f * x * fmaf(kC * 0.044715f, x * x, kC);
-  return x * sigmoid(two_u);
-}
-
 // LDS stage geometry for a K depth of BK 16-bit elements.  A stage row (one row
 // of A or of W) is BK*2 bytes = BK/8 chunks of 16 bytes.  A ds_read_b128 is
 // served 16 lanes at a time across 64 four-byte banks (256 bytes), which hold
@@ -287,39 +259,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Epilogue code prefetch.  Every launch starts with cold instruction caches,
-// and the epilogue runs once per tile after the K loop, so its first execution
-// on a CU takes one instruction-cache miss per 64-byte line in sequence.  The
-// K loop pulls the epilogue's machine code into L2 with ordinary vector loads
-// shortly before it ends, so those misses are served by L2.  The byte range is
-// the epilogue's own code, [label 7, label 8) of this function, computed by the
-// assembler relative to s_getpc_b64 (which returns the address of the next
-// instruction, the s_mov).
-struct CodeSpan {
-  uint64_t pc;   // address of the s_mov after s_getpc
-  int32_t off;   // epilogue start - pc
-  int32_t len;   // epilogue bytes
-};
-
-__device__ __forceinline__ CodeSpan epilogue_code_span() {
-  CodeSpan c;
-  asm volatile("s_getpc_b64 %0\n\ts_mov_b32 %1, 7f-.\n\ts_mov_b32 %2, 8f-7f"
-               : "=s"(c.pc), "=s"(c.off), "=s"(c.len));
-  return c;
-}
-
-// One dword from each of 64 consecutive 64-byte lines of part `part` of the
-// span.  The buffer's size is the span, so loads past its end return zero.  The
-// destination register must stay live until a vmcnt(0) wait: the load is not
-// visible to the compiler's wait-count tracking (which can then only over-wait).
-__device__ __forceinline__ void prefetch_code(const CodeSpan& c, int part, int lane, uint32_t& junk) {
-  if (c.off <= 0 || c.len <= 0 || c.len >= (1 << 22)) return;
-  const __amdgpu_buffer_rsrc_t r =
-      make_rsrc(reinterpret_cast<const void*>(c.pc + (uint64_t)c.off), (uint32_t)c.len);
-  const uint32_t voff = (uint32_t)(part * 64 + lane) * 64u;
-  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(junk) : "v"(voff), "s"(r) : "memory");
-}
-
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
 // wherever an accumulator array is indexed, so every index is a constant and
 // the arrays stay in registers whatever the unroller decides.
@@ -329,6 +268,75 @@ __device__ __forceinline__ void static_for(F&& f) {
     f(std::integral_constant<int, B>{});
     static_for<B + 1, E>(f);
   }
+}
+
+// The activations over G independent elements, evaluated one step at a time
+// across all of them, with a scheduling barrier between steps: a dependent
+// instruction issues G instructions after its input instead of right behind it,
+// which a lone wave on a SIMD (nothing else to issue while a dependent VALU op
+// waits) needs to keep the VALU busy.
+__device__ __forceinline__ void step_boundary() { __builtin_amdgcn_sched_barrier(0); }
+
+// GELU (approximate='none'): x * Phi(x), with Phi(x) = 0.5 + xc * Q(xc^2),
+// xc = clamp(x, +-3 sqrt 2), Q in Horner form.
+template <int G>
+__device__ __forceinline__ void gelu_erf_n(float* v) {
+  float xc[G], t[G], q[G];
+  static_for<0, G>([&](auto e) { xc[e] = __builtin_amdgcn_fmed3f(v[e], -kPhiClamp, kPhiClamp); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { t[e] = xc[e] * xc[e]; });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(kPhiQ8, t[e], kPhiQ7); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(q[e], t[e], kPhiQ6); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(q[e], t[e], kPhiQ5); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(q[e], t[e], kPhiQ4); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(q[e], t[e], kPhiQ3); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(q[e], t[e], kPhiQ2); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(q[e], t[e], kPhiQ1); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(q[e], t[e], kPhiQ0); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { q[e] = fmaf(xc[e], q[e], 0.5f); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { v[e] = v[e] * q[e]; });
+}
+
+// Logistic function from the hardware exp2 and reciprocal (about 1 ulp each):
+// 1 / (1 + 2^(-x log2 e)).
+template <int G>
+__device__ __forceinline__ void sigmoid_n(float* v) {
+  float d[G];
+  static_for<0, G>([&](auto e) { d[e] = -1.4426950408889634f * v[e]; });
+  step_boundary();
+  static_for<0, G>([&](auto e) { d[e] = __builtin_amdgcn_exp2f(d[e]); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { d[e] = 1.0f + d[e]; });
+  step_boundary();
+  static_for<0, G>([&](auto e) { v[e] = __builtin_amdgcn_rcpf(d[e]); });
+}
+
+// GELU, approximate='tanh': 0.5 x (1 + tanh(u)) with u = sqrt(2/pi)(x + 0.044715 x^3)
+// (Hendrycks & Gimpel 2016).  Since 0.5 (1 + tanh(u)) = sigmoid(2u), this is
+// x * sigmoid(2u), 2u = 2x * (sqrt(2/pi) + sqrt(2/pi) 0.044715 x^2).
+template <int G>
+__device__ __forceinline__ void gelu_tanh_n(float* v) {
+  constexpr float kC = 0.79788456080286536f;  // sqrt(2/pi)
+  float u[G];
+  static_for<0, G>([&](auto e) { u[e] = v[e] * v[e]; });
+  step_boundary();
+  static_for<0, G>([&](auto e) { u[e] = fmaf(kC * 0.044715f, u[e], kC); });
+  step_boundary();
+  static_for<0, G>([&](auto e) { u[e] = (2.0f * v[e]) * u[e]; });
+  step_boundary();
+  sigmoid_n<G>(u);
+  step_boundary();
+  static_for<0, G>([&](auto e) { v[e] = v[e] * u[e]; });
 }
 
 // Byte address of 8-byte unit u (four 16-bit elements) of row r in an LDS
@@ -353,10 +361,11 @@ __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, 
 // ---------------------------------------------------------------------------
 
 // SCHED selects the K-loop schedule: 0 lock-step waves, 1 ping-pong (8 waves,
-// two per SIMD), 2 one wave per SIMD with the barrier between the stage's two
-// MFMA k-steps (4 waves, 128x128 wave tiles, accumulators in AGPRs).
+// two per SIMD), 3 one wave per SIMD (4 waves, 128x128 wave tiles, accumulators
+// in AGPRs) with two deep stages (BK=64) and the barrier before each stage's
+// last k-step.
 template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T>
-__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED == 2 ? 1 : 2)))
+__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED == 3 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   KDesc& d = *(KDesc*)(__builtin_amdgcn_kernarg_segment_ptr());
   using G = StageGeom<BK>;
@@ -384,12 +393,6 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const CodeSpan code = epilogue_code_span();
-  uint32_t code_junk = 0;
-  // Code prefetch part of this wave: the workgroups an XCD runs together (the
-  // hardware deals them round-robin over the 8 XCDs) split the span between
-  // their first four waves, 64 lines each.
-  const int code_part = ((blockIdx.x >> 3) & 31) * 4 + (wave & 3);
   const int wm = wave / WN;
   const int wn = wave % WN;
 
@@ -536,68 +539,75 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
     };
-    if constexpr (SCHED == 2) {
-      // One wave per SIMD.  Stage k is consumed in two MFMA k-steps:
-      //   (1) k-step 0's MFMAs run while k-step 1's fragments are read and the
-      //       DMA of stage k+S-1 is issued (into the slot of stage k-1);
-      //   (2) this wave's LDS reads of stage k are complete and its DMAs of
-      //       stage k+1 have landed; then the workgroup barrier, after which
-      //       stage k+1 is visible to every wave;
-      //   (3) k-step 1's MFMAs (fragments already in registers) run while stage
-      //       k+1's k-step 0 fragments are read.
-      // The MFMA pipe drains only for the barrier itself.  A DMA issued in
-      // iteration k overwrites the slot of stage k-1, whose last reads every
-      // wave completed before the barrier of iteration k-1.
-      static_assert(KS == 2, "two MFMA k-steps per stage");
-      i32x4_t f0a[NI], f0b[NJ], f1a[NI], f1b[NJ];
-      auto read = [&](const char* st, int ks, i32x4_t* fa, i32x4_t* fb) {
+    if constexpr (SCHED == 3) {
+      // One wave per SIMD, two stages of BK=64 (four MFMA k-steps each).  Stage k:
+      //   k-steps 0..2: MFMAs of k-step s while k-step s+1's fragments are read;
+      //   then this wave's LDS reads are complete and its DMA of stage k+1 has
+      //   landed, and the workgroup barrier: stage k+1 is visible, and no wave
+      //   reads stage k's slot any more (k-step 3's fragments are in registers);
+      //   k-step 3: MFMAs while the DMA of stage k+2 is issued into stage k's slot
+      //   and stage k+1's k-step 0 fragments are read.
+      // One barrier per 64 MFMAs per wave; the DMA has three k-steps plus one to
+      // land.
+      static_assert(S == 2 && KS == 4, "two stages of four k-steps");
+      i32x4_t fa[2][NI], fb[2][NJ];
+      auto read = [&](const char* st, int ks, auto buf) {
         const int chunk = ((2 * ks + khalf) ^ swz) << 4;
         static_for<0, NI>([&](auto i) {
-          fa[i] = *reinterpret_cast<const i32x4_t*>(st + fa_row + 32 * i * RB + chunk);
+          fa[buf][i] = *reinterpret_cast<const i32x4_t*>(st + fa_row + 32 * i * RB + chunk);
         });
         static_for<0, NJ>([&](auto j) {
-          fb[j] = *reinterpret_cast<const i32x4_t*>(st + fb_row + 32 * j * RB + chunk);
+          fb[buf][j] = *reinterpret_cast<const i32x4_t*>(st + fb_row + 32 * j * RB + chunk);
         });
       };
-      auto mma = [&](const i32x4_t* fa, const i32x4_t* fb) {
+      auto mma = [&](auto buf) {
         static_for<0, NI>([&](auto i) {
-          static_for<0, NJ>([&](auto j) { acc[i][j] = mfma32<T>(fa[i], fb[j], acc[i][j]); });
+          static_for<0, NJ>([&](auto j) { acc[i][j] = mfma32<T>(fa[buf][i], fb[buf][j], acc[i][j]); });
         });
       };
-      static_for<0, S - 1>([&](auto p) {
-        if (p < nk) load_stage(p, p);
-      });
-      int issued = min(nk, S - 1);
-      // This wave's DMAs of stage `need` have landed (the later stages may stay in flight).
-      auto wait_stage = [&](int need) {
-        if (need >= nk) return;
-        const int allowed = min(max(issued - need - 1, 0), S - 2);
-        static_for<0, S - 1>([&](auto a) {
-          if (allowed == a) wait_vmcnt<LPS * a>();
+      // Interleave hints for one k-step: NI*NJ MFMAs with `reads` LDS reads and
+      // `dmas` DMA issues spread between them.
+      auto interleave = [&](auto reads, auto dmas) {
+        constexpr int NM = NI * NJ;
+        static_for<0, NM>([&](auto q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          if constexpr (q < decltype(reads)::value) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if constexpr (q < decltype(dmas)::value) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         });
       };
-      wait_stage(0);
+      using Z = std::integral_constant<int, 0>;
+      using O = std::integral_constant<int, 1>;
+      using R = std::integral_constant<int, NI + NJ>;
+      using D = std::integral_constant<int, LPS>;
+      load_stage(0, 0);
+      if (nk > 1) load_stage(1, 1);
+      if (nk > 1)
+        wait_vmcnt<LPS>();
+      else
+        wait_vmcnt<0>();
       barrier();
-      read(smem, 0, f0a, f0b);
-      int slot = 0;
+      read(smem, 0, Z{});
       for (int k = 0; k < nk; ++k) {
-        const char* st = smem + slot * STAGE;
-        if (++slot == S) slot = 0;
-        // Every DMA has landed at the start of the last iteration.
-        if (k == nk - 1) prefetch_code(code, code_part, lane, code_junk);
-        read(st, 1, f1a, f1b);
-        if (k + S - 1 < nk) {
-          int ls = slot + S - 2;
-          if (ls >= S) ls -= S;
-          load_stage(k + S - 1, ls);
-        }
-        issued = min(nk, k + S);
-        mma(f0a, f0b);
+        const char* st = smem + (k & 1) * STAGE;
+        read(st, 1, O{});
+        mma(Z{});
+        interleave(R{}, Z{});
+        read(st, 2, Z{});
+        mma(O{});
+        interleave(R{}, Z{});
+        read(st, 3, O{});
+        mma(Z{});
+        interleave(R{}, Z{});
         wait_lgkmcnt0();
-        wait_stage(k + 1);
+        if (k + 1 < nk) wait_vmcnt<0>();  // this wave's DMA of stage k+1 (stage k+2 is not issued yet)
         barrier();
-        if (k + 1 < nk) read(smem + slot * STAGE, 0, f0a, f0b);
-        mma(f1a, f1b);
+        // Straight-line code, so the DMA and reads interleave with the MFMAs: past
+        // the last stage the DMA reads nothing (zero fill of a slot that is not
+        // read again) and the fragments read are unused.
+        load_stage(k + 2, k & 1);
+        read(smem + ((k + 1) & 1) * STAGE, 0, Z{});
+        mma(O{});
+        interleave(R{}, D{});
       }
     } else if constexpr (SCHED == 1) {
       // Ping-pong: waves 0-3 and 4-7 (one of each per SIMD) alternate between a
@@ -639,19 +649,11 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       };
       // End of a phase: this wave's DMAs of stage `need` (read by the next
       // memory phase) have landed, then the workgroup barrier.
-      // A code prefetch issued after the last DMA (pf = 1) is the newest vector
-      // memory op: one more op may stay outstanding.
-      int pf = 0;
       auto end_phase = [&](int need) {
         if (need < nk) {
           const int allowed = min(max(issued - need - 1, 0), S - 1);
           static_for<0, S>([&](auto a) {
-            if (allowed == a) {
-              if (pf)
-                wait_vmcnt<LPS * a + 1>();
-              else
-                wait_vmcnt<LPS * a>();
-            }
+            if (allowed == a) wait_vmcnt<LPS * a>();
           });
         }
         // sched_barrier(0) keeps the scheduler from moving any instruction
@@ -667,12 +669,6 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         for (int k = 0; k < nk; ++k) {
           mem(k);
           end_phase(k);
-          // Two stages before the end, every DMA has been issued: the prefetch
-          // has a stage of MFMAs to land in before the epilogue.
-          if (k == max(nk - 2, 0)) {
-            prefetch_code(code, code_part, lane, code_junk);
-            pf = 1;
-          }
           comp();
           end_phase(k + 1);
         }
@@ -714,13 +710,10 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           if (nslot >= S) nslot -= S;
           load_stage(kt + S - 1, nslot);
         }
-        // Every DMA has landed at the start of the last iteration.
-        if (kt == nk - 1) prefetch_code(code, code_part, lane, code_junk);
         compute(smem + slot * STAGE);
         if (++slot == S) slot = 0;
       }
     }
-    asm volatile("7:");  // start of the prefetched epilogue code
     for (int oi = 0; oi < d.n_operands; ++oi) {
       const int fl = d.operands[oi].reserved;
       if (!(fl & kFlagAux) || tid >= (d.operands[oi].stride_m == 0 ? BN : BM)) continue;
@@ -731,9 +724,6 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       });
     }
     __syncthreads();  // the epilogue reuses the stage LDS; the vector slots are written
-    // The barrier's release fence waited for every vector memory op (vmcnt(0)),
-    // the code prefetch included: its register is free from here on.
-    asm volatile("" ::"v"(code_junk));
 
     // ---------------------------------------------------------------------
     // Epilogue.  In accumulator block (i,j), register r of this lane holds
@@ -772,13 +762,25 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       const void* optr = d.operands[staged].ptr;
       const int64_t osm = d.operands[staged].stride_m;
       const __amdgpu_buffer_rsrc_t r = make_rsrc(optr, (uint32_t)(d.operands[staged].extent * 2));
-      static_for<0, BM / RPP>([&](auto p) {
-        const int rl = p * RPP + crow;
-        const int m = m0 + rl, n = n0 + 8 * cchk;
-        const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * osm + n) * 2) : kOOB;
-        i32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-        if (rl & 1) x = swap_halves(x);
-        *reinterpret_cast<i32x4_t*>(stg + stage_chunk<BN>(rl, cchk)) = x;
+      // Batches of 8 passes: the loads of a batch are all in flight before the
+      // first LDS write.  Offsets in 32-bit arithmetic (exact for every in-range
+      // element: the host bounds the operand's span below 2 GiB) and selected,
+      // not branched on, so nothing serializes the loads.
+      constexpr int NP = BM / RPP;
+      constexpr int PB = NP < 8 ? NP : 8;
+      static_assert(NP % PB == 0, "pass batches");
+      static_for<0, NP / PB>([&](auto b) {
+        i32x4_t x[PB];
+        static_for<0, PB>([&](auto q) {
+          const int rl = (b * PB + q) * RPP + crow;
+          const int m = m0 + rl, n = n0 + 8 * cchk;
+          const uint32_t o32 = ((uint32_t)m * (uint32_t)osm + (uint32_t)n) * 2u;
+          x[q] = __builtin_amdgcn_raw_buffer_load_b128(r, (m < M && n < N) ? o32 : kOOB, 0, 0);
+        });
+        static_for<0, PB>([&](auto q) {
+          const int rl = (b * PB + q) * RPP + crow;
+          *reinterpret_cast<i32x4_t*>(stg + stage_chunk<BN>(rl, cchk)) = (rl & 1) ? swap_halves(x[q]) : x[q];
+        });
       });
     }
     if (staged >= 0) __syncthreads();
@@ -790,6 +792,14 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // per column block.  Carrying one column block (not all of them) through the
     // runtime op loop keeps the loop's live values within the register file.
     const bool use_stage_out = d.out.ptr != nullptr && (d.out.reserved & kFlagStage) && !col_red;
+    const bool out_bf16 = d.out.dtype == FUSEML_BF16;
+    float rs[NJ], rmx[NJ];  // row partials (sum, max) of this lane's rows
+    static_for<0, NJ>([&](auto j) {
+      rs[j] = 0.0f;
+      rmx[j] = -INFINITY;
+    });
+    float* red_sum = reinterpret_cast<float*>(smem);
+    float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
     static_for<0, NI>([&](auto i) {
       for (int o = 0; o < d.n_ops; ++o) {
         // Lane coordinates through an opaque copy: the per-block addresses derived
@@ -883,15 +893,25 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           case FUSEML_OP_RELU:
             FUSEML_EACH(v > 0.0f ? v : 0.0f);
             break;
+#define FUSEML_EACH_N(fn)                                \
+  static_for<0, NJ>([&](auto j) {                        \
+    static_for<0, 2>([&](auto h) {                       \
+      float x8[8];                                       \
+      static_for<0, 8>([&](auto e) { x8[e] = acc[i][j][8 * h + e]; }); \
+      fn<8>(x8);                                         \
+      static_for<0, 8>([&](auto e) { acc[i][j][8 * h + e] = x8[e]; }); \
+    });                                                  \
+  })
           case FUSEML_OP_GELU_ERF:
-            FUSEML_EACH(gelu_erf(v));
+            FUSEML_EACH_N(gelu_erf_n);
             break;
           case FUSEML_OP_GELU_TANH:
-            FUSEML_EACH(gelu_tanh(v));
+            FUSEML_EACH_N(gelu_tanh_n);
             break;
           case FUSEML_OP_SIGMOID:
-            FUSEML_EACH(sigmoid(v));
+            FUSEML_EACH_N(sigmoid_n);
             break;
+#undef FUSEML_EACH_N
           case FUSEML_OP_SCALE:
             FUSEML_EACH(v * sc);
             break;
@@ -909,18 +929,12 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
             break;
         }
       }
-    });
 
-    // Unstaged output stores and reduction partials over the final values.
-    float rs[NJ], rmx[NJ];
-    static_for<0, NJ>([&](auto j) {
-      rs[j] = 0.0f;
-      rmx[j] = -INFINITY;
-    });
-    float* red_sum = reinterpret_cast<float*>(smem);
-    float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
-
-    static_for<0, NI>([&](auto i) {
+      // The column block's final values: unstaged stores, reduction partials and
+      // the staged output, before the next column block, so that its NJ*16
+      // values stay in registers from the first op to the LDS write.  The staged
+      // output overwrites the staged operand in place: each 8-byte unit is read
+      // (above) and written (here) by the same lane.
       float cs[16], cmx[16];
       static_for<0, 16>([&](auto r) {
         cs[r] = 0.0f;
@@ -929,6 +943,19 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       static_for<0, NJ>([&](auto j) {
         const int m = mw + 32 * j;
         const int nb = nw + 32 * i;
+        if (use_stage_out) {
+          const int r_loc = wm * TM + 32 * j + l32;
+          const int u0 = (wn * TN + 32 * i) / 4 + khalf;
+          static_for<0, 4>([&](auto g) {
+            uint32_t h[4];
+            static_for<0, 4>([&](auto e) {
+              const float x = acc[i][j][4 * g + e];
+              h[e] = out_bf16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+            });
+            *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
+                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+          });
+        }
         if (d.out.ptr != nullptr && !use_stage_out) {
           static_for<0, 4>([&](auto g) {
             const float x[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
@@ -973,25 +1000,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       }
     });
 
-    // (3) Staged output: registers -> LDS (16-bit), then whole-row 16-byte stores.
+    // (3) Staged output: the LDS tile (written above), drained by whole-row
+    // 16-byte stores.
     if (use_stage_out) {
-      if (staged >= 0) __syncthreads();  // every wave is done reading the staged operand
-      const bool bf = d.out.dtype == FUSEML_BF16;
-      static_for<0, NI>([&](auto i) {
-        static_for<0, NJ>([&](auto j) {
-          const int r_loc = wm * TM + 32 * j + l32;
-          const int u0 = (wn * TN + 32 * i) / 4 + khalf;
-          static_for<0, 4>([&](auto g) {
-            uint32_t h[4];
-            static_for<0, 4>([&](auto e) {
-              const float x = acc[i][j][4 * g + e];
-              h[e] = bf ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
-            });
-            *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
-                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-          });
-        });
-      });
       __syncthreads();
       // A short loop rather than BM/RPP unrolled passes: this code runs once per
       // tile, and its size is paid in instruction-cache misses.
@@ -1008,7 +1019,6 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       }
     }
 
-    asm volatile("8:");  // end of the prefetched epilogue code
     if (d.reduce_mask == 0) return;
     if (row_red) {
       if (use_stage_out) __syncthreads();  // LDS staging tile is being drained
@@ -1067,30 +1077,30 @@ struct TileConfig {
   }
 };
 
-constexpr TileConfig kQuad = {256, 256, 32, 4, 2, 2, 2};   // 4 waves (1/SIMD), 128x128 wave tiles, 132 KB LDS
 constexpr TileConfig kLarge = {256, 256, 32, 4, 2, 4, 1};  // 8 waves ping-pong, 132 KB LDS, 1 WG/CU
-constexpr TileConfig kLargeL = {256, 256, 32, 4, 2, 4, 0}; // same tile, lock-step waves
-constexpr TileConfig kWide = {128, 256, 32, 3, 2, 2, 0};   // 4 waves, 76 KB LDS, 2 WG/CU
-constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2, 0};  // 4 waves, 66 KB LDS, 2 WG/CU
+constexpr TileConfig kDeep = {256, 256, 64, 2, 2, 2, 3};   // 4 waves (1/SIMD), BK=64 x 2 stages, 132 KB LDS
+constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2, 0};  // 4 waves lock-step, 66 KB LDS, 2 WG/CU
 
 constexpr int64_t kMaxBytes = (int64_t)1 << 31;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 TileConfig choose_config(const fuseml_gemm_desc& d) {
-  // FUSEML_HIP_TILE=quad|large|lockstep|wide|small pins a variant (tuning sweeps).
+  // FUSEML_HIP_TILE=large|deep|small pins a variant (tuning sweeps).
   if (const char* force = getenv("FUSEML_HIP_TILE")) {
-    if (!strcmp(force, "quad")) return kQuad;
     if (!strcmp(force, "large")) return kLarge;
-    if (!strcmp(force, "lockstep")) return kLargeL;
-    if (!strcmp(force, "wide")) return kWide;
+    if (!strcmp(force, "deep")) return kDeep;
     if (!strcmp(force, "small")) return kSmall;
   }
   // A 256x256 tile keeps the LDS traffic per MFMA low enough for the MFMA pipe
   // to stay busy; below one full wave of 256-tile work the 128x128 variant
-  // fills more CUs.
+  // fills more CUs.  Of the two 256x256 schedules, the one-wave-per-SIMD one
+  // has the faster K loop but the slower epilogue (no second wave on a SIMD to
+  // overlap its latencies): it wins once K is long enough to amortize that,
+  // about K >= 8192 on the measured shapes.
   const int64_t large_tiles = cdiv(d.M, 256) * cdiv(d.N, 256);
-  return large_tiles >= 128 ? kLarge : kSmall;
+  if (large_tiles < 128) return kSmall;
+  return d.K >= 8192 ? kDeep : kLarge;
 }
 
 bool check_output(const fuseml_output& o, const fuseml_gemm_desc& d, const char* what) {
@@ -1333,14 +1343,10 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
   }
 
   const TileConfig c = choose_config(d);
-  if (c.bm == kQuad.bm && c.bn == kQuad.bn && c.sched == kQuad.sched)
-    e = launch_variant<kQuad>(d, stream);
-  else if (c.bm == kLarge.bm && c.bn == kLarge.bn && c.sched == kLarge.sched)
+  if (c.sched == kDeep.sched)
+    e = launch_variant<kDeep>(d, stream);
+  else if (c.sched == kLarge.sched)
     e = launch_variant<kLarge>(d, stream);
-  else if (c.bm == kLargeL.bm && c.bn == kLargeL.bn)
-    e = launch_variant<kLargeL>(d, stream);
-  else if (c.bm == kWide.bm && c.bn == kWide.bn)
-    e = launch_variant<kWide>(d, stream);
   else
     e = launch_variant<kSmall>(d, stream);
   if (e != hipSuccess) {

@@ -155,6 +155,72 @@ def test_reductions_parity(axis, shape):
     _check_red(mean, ref["mean"], np.abs(v).mean(axis=axis), "mean")
 
 
+# ---------------------------------------------------------------------------
+# Every kernel variant (tile size and K-loop schedule), forced through
+# FUSEML_HIP_TILE, which the library reads at each launch.  The automatic choice
+# picks the 256x256 variants only at large sizes, so these cases are what pins
+# the ping-pong ("large") and one-wave-per-SIMD ("deep", BK=64) schedules on
+# every chain, on ragged edges and on K that ends mid-stage.
+# ---------------------------------------------------------------------------
+
+VARIANTS = ["large", "deep", "small"]
+VARIANT_SHAPES = [
+    (600, 1030, 200),   # ragged M and N, K ends mid-stage (BK=32 and BK=64)
+    (257, 512, 72),     # one row past a 256 tile, K = one BK=64 stage + 8
+    (512, 520, 2048),   # several tiles, many stages, N % 8 == 0 but not % 256
+    (64, 96, 40),       # smaller than one tile, a single stage
+]
+
+
+@pytest.fixture
+def forced_variant(request, monkeypatch):
+    monkeypatch.setenv("FUSEML_HIP_TILE", request.param)
+    return request.param
+
+
+@pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
+@pytest.mark.parametrize("chain", sorted(CHAINS))
+@pytest.mark.parametrize("shape", VARIANT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_variant_chain_parity(forced_variant, chain, shape):
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=21)
+    ops = _operands(M, N, dtype, seed=22)
+    inputs = ops + [a, w.t()]
+    left, right = len(ops), len(ops) + 1
+    steps = CHAINS[chain]
+    spec = _spec(left=left, right=right, ops=steps, out_dtype=dtype)
+    print(f"case variant={forced_variant} chain={chain} shape={shape}", flush=True)
+    out = _launcher(spec, len(inputs))(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], left, right, steps)["tile"]
+    _check_tile(out, ref, f"{forced_variant} {chain} {shape}")
+
+
+@pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
+@pytest.mark.parametrize("axis", [1, 0])
+def test_variant_reductions_parity(forced_variant, axis):
+    M, N, K = 600, 1030, 200
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=23)
+    bias = (torch.rand(N, generator=_gen(24)) - 0.5).to(dtype)
+    inputs = [bias, a, w.t()]
+    steps = [("add", 0, 1.0), ("gelu_erf", -1, 1.0)]
+    spec = _spec(left=1, right=2, ops=steps, out_dtype=dtype, store_tile=True,
+                 reductions=("sum", "amax", "mean"), reduce_axis=axis,
+                 reduce_dtypes=(torch.float32,) * 3,
+                 outputs=(("tile",), ("red", "sum"), ("red", "amax"), ("red", "mean")))
+    print(f"case variant={forced_variant} reductions axis={axis}", flush=True)
+    tile, s, mx, mean = _launcher(spec, 3)(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], 1, 2, steps, ("sum", "amax", "mean"), axis)
+    v = ref["tile"]
+    _check_tile(tile, v, f"{forced_variant} tile")
+    _check_red(s, ref["sum"], np.abs(v).sum(axis=axis), "sum")
+    _check_red(mx, ref["amax"], np.abs(v).max(axis=axis), "amax")
+    _check_red(mean, ref["mean"], np.abs(v).mean(axis=axis), "mean")
+
+
 def test_escape_store_and_tile_with_reductions():
     """mm -> relu (escapes) -> row sum/amax/mean: the C4 group shape, small."""
     M, N, K = 320, 640, 256
