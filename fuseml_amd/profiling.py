@@ -28,8 +28,12 @@ COPY_KERNEL_HINT = "copyBuffer"
 
 
 def _short(name: str) -> str:
-    if "gemm_epilogue_kernel" in name:
-        return "gemm_epilogue_kernel" + name[name.index("ILi"):].split("EEv")[0].replace("ILi", "<").replace("ELi", ",")
+    """gemm_epilogue_kernel<BM,BN,BK,S,WM,WN,SCHED,dtype> from the mangled name."""
+    if "gemm_epilogue_kernel" in name and "ILi" in name:
+        args = name[name.index("ILi") + 3:].split("EEv")[0]
+        ints, _, tail = args.rpartition("E")
+        dtype = {"DF16b": "bf16", "DF16_": "f16"}.get(tail, tail)
+        return "gemm_epilogue_kernel<" + ints.replace("ELi", ",") + "," + dtype + ">"
     return name[:60]
 
 
