@@ -130,10 +130,12 @@ class FuseMLCompiler:
     """``torch.compile`` backend fusing addmm/mm epilogue chains into HIP kernels."""
 
     def __init__(self, registry: Any = None, *, fuse_sibling_reductions: bool = False,
+                 fuse_leading_views: bool = False,
                  min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
                  require_gfx950: bool = True) -> None:
         self.registry = registry
         self.fuse_sibling_reductions = fuse_sibling_reductions
+        self.fuse_leading_views = fuse_leading_views
         self.min_output_elements = min_output_elements
         self.require_gfx950 = require_gfx950
         self.fusion_candidates: List[torch.fx.Node] = []
@@ -182,7 +184,8 @@ class FuseMLCompiler:
         if not fusible:
             raise _NoFusionPossible("every trigger is below the fusion threshold or unsupported")
 
-        fpass = FuseMLFusionPass(gm, self.registry, fuse_sibling_reductions=self.fuse_sibling_reductions)
+        fpass = FuseMLFusionPass(gm, self.registry, fuse_sibling_reductions=self.fuse_sibling_reductions,
+                                 fuse_leading_views=self.fuse_leading_views)
         gm = fpass.run(example_inputs)
         placeholders = [n for n in gm.graph.nodes
                         if n.op == "call_function" and n.target is fuseml_fused_kernel_placeholder]

@@ -91,6 +91,11 @@ class EpilogueSpec:
     extra_dtypes: Tuple[torch.dtype, ...] = ()
     # Return order: ("tile",), ("red", name) or ("extra", k).
     outputs: Tuple[Tuple[Any, ...], ...] = (("tile",),)
+    # N-D groups (the GEMM's [M,N] result viewed as [*lead, N]): the value shape
+    # each such operand is broadcast against, as (input index, shape) pairs, and
+    # the shape each returned value is viewed as (None: the natural [M,N]/[M]/[N]).
+    operand_shapes: Tuple[Tuple[int, Tuple[int, ...]], ...] = ()
+    output_shapes: Tuple[Optional[Tuple[int, ...]], ...] = ()
 
     def chain(self) -> List[Tuple[str, int, float]]:
         """Plain-data form of the op chain, as consumed by the CPU oracle."""
@@ -122,21 +127,54 @@ def _is_node(x: Any) -> bool:
     return isinstance(x, torch.fx.Node)
 
 
+def _node_shape(node: Any) -> Optional[Tuple[int, ...]]:
+    meta = getattr(node, "meta", {}) or {}
+    for key in ("tensor_meta", "val"):
+        v = meta.get(key)
+        if v is not None and hasattr(v, "shape"):
+            try:
+                return tuple(int(d) for d in v.shape)
+            except (TypeError, ValueError):  # symbolic sizes
+                return None
+    return None
+
+
+def leading_dim_view(src_shape: Optional[Tuple[int, ...]], out_shape: Optional[Tuple[int, ...]]) -> bool:
+    """A view between [*a, N] and [*b, N] with prod(a) == prod(b): only the row
+    (M) dimension is split or merged, so the row-major [M,N] layout is unchanged."""
+    if not src_shape or not out_shape or len(src_shape) < 2 or len(out_shape) < 2:
+        return False
+    if src_shape[-1] != out_shape[-1]:
+        return False
+    pa = pb = 1
+    for d in src_shape[:-1]:
+        pa *= d
+    for d in out_shape[:-1]:
+        pb *= d
+    return pa == pb
+
+
 def _group_args(group: Any, node: torch.fx.Node) -> tuple:
     snap = getattr(group, "node_args_snapshot", None) or {}
     return tuple(snap.get(node.name, node.args))
 
 
-def reduction_axis(dims: Any) -> int:
+def reduction_axis(dims: Any, ndim: int = 2) -> int:
     """Map reduction dims of a 2-D [M,N] value to a tile axis.
 
     Follows fuseml/codegen/kernel_generator.py:1909-1931: dims are normalised
     modulo 2; any 1 means "reduce along N" (axis 1, result [M]); otherwise axis 0.
+    An N-D value ([*lead, N], ndim > 2) supports only the last dimension
+    (axis 1, result [*lead]).
     """
     if dims is None:
         dims = [-1]
     if isinstance(dims, int):
         dims = [dims]
+    if ndim > 2:
+        if sorted({int(d) % ndim for d in dims}) != [ndim - 1]:
+            raise UnsupportedGroup("an N-D value is reduced only over its last dimension")
+        return 1
     norm = [int(d) % 2 for d in dims]
     if len(set(norm)) > 1:
         raise UnsupportedGroup("reduction over both axes is not a single-axis row/column reduction")
@@ -184,6 +222,20 @@ def spec_from_group(group: Any) -> EpilogueSpec:
     red_axis: Optional[int] = None
     red_source: Optional[int] = None
     tile_node = base
+    # Shape of the value the ops act on: the GEMM's [M,N], or [*lead, N] after a
+    # leading-dimension view.  Operands of ops on an N-D value are broadcast
+    # against that shape (the launcher merges it back to [M,N]).
+    base_shape = _node_shape(base)
+    cur_shape = base_shape
+    operand_shapes: Dict[int, Tuple[int, ...]] = {}
+
+    def note_operand(k: int) -> None:
+        if cur_shape is None or len(cur_shape) == 2:
+            if k in operand_shapes:
+                raise UnsupportedGroup("operand broadcast against values of different ranks")
+            return
+        if operand_shapes.setdefault(k, cur_shape) != cur_shape:
+            raise UnsupportedGroup("operand broadcast against values of different shapes")
 
     for node in group.fused_nodes:
         t = node.target
@@ -197,7 +249,8 @@ def spec_from_group(group: Any) -> EpilogueSpec:
             keepdim = bool(args[2]) if len(args) > 2 else bool(node.kwargs.get("keepdim", False))
             if keepdim:
                 raise UnsupportedGroup("keepdim=True reductions are not fused")
-            ax = reduction_axis(args[1] if len(args) > 1 else node.kwargs.get("dim"))
+            ax = reduction_axis(args[1] if len(args) > 1 else node.kwargs.get("dim"),
+                                len(cur_shape) if cur_shape else 2)
             if red_axis is not None and ax != red_axis:
                 raise UnsupportedGroup("sibling reductions along different axes")
             red_axis = ax
@@ -207,6 +260,13 @@ def spec_from_group(group: Any) -> EpilogueSpec:
         if reductions:
             raise UnsupportedGroup("op after a reduction")
         if t in TRANSPARENT_TARGETS:
+            new_shape = _node_shape(node)
+            if new_shape != cur_shape:
+                if not leading_dim_view(cur_shape, new_shape):
+                    raise UnsupportedGroup(f"{node.name}: view changes more than the row dimension")
+                cur_shape = new_shape
+            if id(node) in escape_idx:  # an escaping view holds the current value
+                ops.append(EpiOp("store", operand=escape_idx[id(node)]))
             continue
         if t in UNARY_TARGETS:
             ops.append(EpiOp(UNARY_TARGETS[t]))
@@ -225,6 +285,7 @@ def spec_from_group(group: Any) -> EpilogueSpec:
                 other = b if a_in else a
                 if _is_node(other):
                     k = input_index(other)
+                    note_operand(k)
                     if is_add:
                         if a_in:  # v + alpha * other
                             ops.append(EpiOp("add", operand=k, scalar=alpha))
@@ -286,6 +347,19 @@ def spec_from_group(group: Any) -> EpilogueSpec:
         k = len(escapes) - 1
         outputs = [("tile",) if o == ("extra", k) else o for o in outputs]
         tile_dtype = extra_dtypes.pop()
+    # Views of the returned values when the group's values are N-D.
+    def view_of(shape: Optional[Tuple[int, ...]]) -> Optional[Tuple[int, ...]]:
+        return shape if shape is not None and len(shape) != 2 else None
+
+    output_shapes: List[Optional[Tuple[int, ...]]] = []
+    for o in outputs:
+        if o[0] == "tile":
+            output_shapes.append(view_of(_node_shape(tile_node) if not reductions else cur_shape))
+        elif o[0] == "extra":
+            output_shapes.append(view_of(_node_shape(escapes[o[1]])))
+        else:
+            output_shapes.append(tuple(cur_shape[:-1]) if cur_shape is not None and len(cur_shape) > 2
+                                 and red_axis == 1 else None)
     return EpilogueSpec(
         left=left,
         right=right,
@@ -297,4 +371,6 @@ def spec_from_group(group: Any) -> EpilogueSpec:
         reduce_dtypes=tuple(dt or torch.float32 for _, dt in reductions),
         extra_dtypes=tuple(extra_dtypes),
         outputs=tuple(outputs),
+        operand_shapes=tuple(sorted(operand_shapes.items())),
+        output_shapes=tuple(output_shapes) if any(sh is not None for sh in output_shapes) else (),
     )

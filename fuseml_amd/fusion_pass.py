@@ -25,6 +25,14 @@ reductions over the same axis (plus any other consumers) absorb all of them;
 the reduced value itself then escapes.  That is the only way the C4 workload
 (``h.sum(-1), h.amax(-1), h.mean(-1)`` of one ``h``) becomes one kernel.
 
+Extension (off by default): ``fuse_leading_views=True`` also absorbs a view,
+reshape or _unsafe_view that only splits or merges the row dimension of the
+group's value ([M,N] <-> [*lead, N], fuseml/passes/fusion_pass.py:537-579 stops
+there), when the node after it is itself absorbed.  ``nn.Linear`` on a [B,S,D]
+activation lowers to ``view -> addmm -> view(B,S,N) -> pointwise``, so this is
+what lets 3-D (transformer-shaped) activations fuse; the trailing flatten that
+feeds the next GEMM stays outside the group.
+
 Each kept group also gets ``eager_module``: a standalone GraphModule of its
 original nodes, the eager fallback for that group.
 """
@@ -47,6 +55,7 @@ from .epilogue import (
     TRANSPARENT_TARGETS,
     TRIGGER_TARGETS,
     UNARY_TARGETS,
+    leading_dim_view,
 )
 from .fusion_group import FusionGroup
 
@@ -108,10 +117,11 @@ class FuseMLFusionPass:
     """Find fusion groups in an ATen graph and replace them with placeholders."""
 
     def __init__(self, graph_module: torch.fx.GraphModule, registry: Any = None,
-                 fuse_sibling_reductions: bool = False) -> None:
+                 fuse_sibling_reductions: bool = False, fuse_leading_views: bool = False) -> None:
         self.graph_module = graph_module
         self.registry = registry
         self.fuse_sibling_reductions = fuse_sibling_reductions
+        self.fuse_leading_views = fuse_leading_views
         self.groups: List[FusionGroup] = []
 
     # ------------------------------------------------------------------
@@ -135,6 +145,25 @@ class FuseMLFusionPass:
         src = node.args[0] if node.args else None
         a, b = _meta_shape(src), _meta_shape(node)
         return a is not None and b is not None and len(a) == 2 and a == b
+
+    _LEADING_VIEW_TARGETS = (aten.view.default, aten._unsafe_view.default, aten.reshape.default)
+
+    def _leading_view(self, node: torch.fx.Node) -> bool:
+        """A row-dimension-only view whose single user the group absorbs next."""
+        if not self.fuse_leading_views or node.target not in self._LEADING_VIEW_TARGETS:
+            return False
+        src = node.args[0] if node.args else None
+        if not leading_dim_view(_meta_shape(src), _meta_shape(node)):
+            return False
+        users = list(node.users)
+        if len(users) != 1 or users[0].op != "call_function":
+            return False
+        u = users[0]
+        if u.target in REDUCTION_TARGETS:
+            return not _keepdim(u)
+        if u.target in INPLACE_TARGETS:
+            return bool(u.args) and u.args[0] is node
+        return u.target in POINTWISE_TARGETS
 
     def _sibling_reductions(self, node: torch.fx.Node) -> List[torch.fx.Node]:
         """Reduction users of `node` that can be fused together (same axis, no keepdim)."""
@@ -197,7 +226,7 @@ class FuseMLFusionPass:
                     absorb(nxt)
                     break
                 if t in TRANSPARENT_TARGETS:
-                    if self._shape_preserving_2d(nxt):
+                    if self._shape_preserving_2d(nxt) or self._leading_view(nxt):
                         absorb(nxt, is_output=False)
                         current = nxt
                         continue

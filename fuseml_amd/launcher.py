@@ -95,7 +95,14 @@ class HipKernelLauncher:
 
     # ------------------------------------------------------------------
     def _operand_tensors(self, inputs: Sequence[torch.Tensor], M: int, N: int) -> List[torch.Tensor]:
-        """Broadcast every add/mul operand to a zero-stride [M,N] view."""
+        """Broadcast every add/mul operand to a zero-stride [M,N] view.
+
+        An operand of an op on an N-D value ([*lead, N], same memory order as
+        [M,N]) is broadcast to that shape first and its leading dimensions
+        merged; when their strides do not merge (e.g. [B,1,N] against
+        [B,S,N]) the merge materialises the broadcast (a copy, still exact).
+        """
+        shapes = dict(self.spec.operand_shapes)
         seen: Dict[int, int] = {}
         ops: List[torch.Tensor] = []
         for op in self.spec.ops:
@@ -103,10 +110,15 @@ class HipKernelLauncher:
                 t = inputs[op.operand]
                 if t.dtype not in _DTYPE_CODE:
                     t = t.to(torch.float32)
-                if t.dim() > 2:
+                shape = shapes.get(op.operand)
+                if shape is not None:
+                    t = t.expand(shape).reshape(M, N)
+                elif t.dim() > 2:
                     raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "operand rank > 2")
+                else:
+                    t = t.expand(M, N)
                 seen[op.operand] = len(ops)
-                ops.append(t.expand(M, N))
+                ops.append(t)
         self._operand_slot = seen
         return ops
 
@@ -201,6 +213,8 @@ class HipKernelLauncher:
                 outs.append(r if dt == torch.float32 else r.to(dt))
             else:
                 outs.append(extras[o[1]])
+        if self.spec.output_shapes:
+            outs = [t if sh is None else t.view(sh) for t, sh in zip(outs, self.spec.output_shapes)]
         return outs[0] if len(outs) == 1 else tuple(outs)
 
     # ------------------------------------------------------------------

@@ -208,3 +208,70 @@ def test_scalar_alpha_and_self_ops_spec():
         ("add", 1.0), ("scale", 0.5), ("add_scalar", 0.125), ("add", -2.0), ("mul_self", 1.0)]
     with torch.no_grad():
         assert torch.allclose(bind_eager(gm, p.groups)(X, y), m(X, y), atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# 3-D activations (opt-in): nn.Linear on [B,S,D] lowers to
+# view -> addmm -> view(B,S,N) -> pointwise; the reference stops at the view.
+# ---------------------------------------------------------------------------
+
+X3 = torch.randn(2, 8, 32)
+
+
+def test_leading_views_off_by_default():
+    p, _ = run_pass(TransformerMLP(32, 64).eval(), (X3,))
+    assert p.groups == []
+
+
+def test_leading_views_opt_in_mlp_block():
+    m = TransformerMLP(32, 64).eval()
+    p, gm = run_pass(m, (X3,), fuse_leading_views=True)
+    assert [targets(g) for g in p.groups] == [
+        [aten.addmm.default, aten.view.default, aten.gelu.default],
+        [aten.addmm.default, aten.view.default, aten.add.Tensor],
+    ]
+    s1, s2 = (spec_from_group(g) for g in p.groups)
+    assert [o.kind for o in s1.ops] == ["add", "gelu_erf"]
+    assert s1.output_shapes == ((2, 8, 64),) and s1.operand_shapes == ()
+    # residual x[2,8,32] is broadcast against the [2,8,32] value; the bias is 1-D
+    res = [i for i, n in enumerate(p.groups[1].inputs) if n.op == "placeholder"][0]
+    assert s2.operand_shapes == ((res, (2, 8, 32)),)
+    assert s2.output_shapes == ((2, 8, 32),)
+    # the flatten feeding the second GEMM stays outside the groups
+    flat = [n for n in gm.graph.nodes if n.target is aten.view.default]
+    assert any(tuple(n.args[1]) == (16, 64) for n in flat)
+    with torch.no_grad():
+        assert torch.allclose(bind_eager(gm, p.groups)(X3), m(X3), atol=1e-5)
+
+
+class _Rows3D(nn.Module):
+    def __init__(self, dim):
+        super().__init__()
+        self.l = nn.Linear(32, 64)
+        self.dim = dim
+
+    def forward(self, x):
+        return torch.relu(self.l(x)).sum(self.dim)
+
+
+def test_leading_views_reduction_last_dim_only():
+    p, gm = run_pass(_Rows3D(-1).eval(), (X3,), fuse_leading_views=True)
+    (g,) = p.groups
+    spec = spec_from_group(g)
+    assert spec.reductions == ("sum",) and spec.reduce_axis == 1
+    assert spec.output_shapes == ((2, 8),)
+    # a reduction over a leading dimension of the 3-D value is not a row reduction
+    p2, _ = run_pass(_Rows3D(1).eval(), (X3,), fuse_leading_views=True)
+    from fuseml_amd.epilogue import UnsupportedGroup
+    with pytest.raises(UnsupportedGroup):
+        spec_from_group(p2.groups[0])
+
+
+def test_leading_dim_view_rule():
+    from fuseml_amd.epilogue import leading_dim_view
+    assert leading_dim_view((16, 64), (2, 8, 64))
+    assert leading_dim_view((2, 8, 64), (16, 64))
+    assert leading_dim_view((2, 8, 64), (4, 4, 64))
+    assert not leading_dim_view((16, 64), (16, 8, 8))     # splits N
+    assert not leading_dim_view((16, 64), (2, 512))       # moves elements across rows
+    assert not leading_dim_view((16, 64), (64,))

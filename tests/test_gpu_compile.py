@@ -147,3 +147,66 @@ def test_forced_fallback_on_gpu(monkeypatch):
     torch.cuda.synchronize()
     assert sum(l.fallback_count for l in {id(l): l for l in be.launchers}.values()) == 2
     assert torch.equal(y, ref)
+
+
+# ---------------------------------------------------------------------------
+# 3-D activations (FuseMLCompiler(fuse_leading_views=True)): x[B,S,D] through
+# nn.Linear lowers to view -> addmm -> view -> pointwise.
+# ---------------------------------------------------------------------------
+
+
+def test_c2_mlp_block_3d_activations():
+    from fuseml_amd.workloads import c2_mlp_block
+
+    wl = c2_mlp_block(scale=1 / 8).to("cuda")      # x[2048,1024] -> [4,512,1024]
+    x3 = wl.inputs[0].view(4, 512, 1024)
+    compiled, be = _compile(wl.model, fuse_leading_views=True)
+    with torch.no_grad():
+        y = compiled(x3)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and be.fusion_strategy == "hip"
+    assert len(be.launchers) == 2 and _launches(be) == 2
+    assert y.shape == (4, 512, 1024)
+    m = wl.model
+    ref = ora_w.transformer_mlp(_f64(wl.inputs[0]), _f64(m.linear1.weight), _f64(m.linear1.bias),
+                                _f64(m.linear2.weight), _f64(m.linear2.bias))
+    _close(y.reshape(2048, 1024), ref, "C2 3-D")
+
+
+class _Gated3D(torch.nn.Module):
+    """relu(l(x)) * g + r with a per-batch gate g[B,1,N] (no single stride over
+    the flattened rows: the launcher materialises it) and a row r[N]; then the
+    last-dimension sum of the result as a second group."""
+
+    def __init__(self, d, n):
+        super().__init__()
+        self.l = torch.nn.Linear(d, n)
+        self.l2 = torch.nn.Linear(d, n)
+
+    def forward(self, x, g, r):
+        y = torch.relu(self.l(x)) * g + r
+        s = torch.sigmoid(self.l2(x)).sum(-1)
+        return y, s
+
+
+def test_3d_broadcast_operands_and_last_dim_reduction():
+    B, S, D, N = 4, 256, 512, 768
+    gen = torch.Generator().manual_seed(31)
+    m = _Gated3D(D, N).to(torch.bfloat16)
+    x = torch.randn(B, S, D, generator=gen).to(torch.bfloat16)
+    g = torch.rand(B, 1, N, generator=gen).to(torch.bfloat16)
+    r = (torch.rand(N, generator=gen) - 0.5).to(torch.bfloat16)
+    m, x, g, r = m.cuda(), x.cuda(), g.cuda(), r.cuda()
+    compiled, be = _compile(m, fuse_leading_views=True, min_output_elements=0)
+    with torch.no_grad():
+        y, s = compiled(x, g, r)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and _launches(be) == 2
+    assert y.shape == (B, S, N) and s.shape == (B, S)
+    W, b = _f64(m.l.weight), _f64(m.l.bias)
+    h = np.maximum(_f64(x) @ W.T + b, 0.0)
+    _close(y, h * _f64(g) + _f64(r), "gated 3-D")
+    v = 1.0 / (1.0 + np.exp(-(_f64(x) @ _f64(m.l2.weight).T + _f64(m.l2.bias))))
+    ref_s = v.sum(-1)
+    err = np.abs(_f64(s) - ref_s)
+    assert (err <= 1e-2 * np.abs(v).sum(-1) + 1e-3).all(), err.max()

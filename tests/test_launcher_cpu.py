@@ -180,3 +180,27 @@ def test_unsupported_gemm_dtype_raises():
 
 def test_name_for_fx():
     assert HipKernelLauncher(EpilogueSpec(0, 1, (), BF), 2).__name__ == "fuseml_fused_kernel"
+
+
+def test_nd_operands_and_output_views():
+    """[*lead, N] groups: operands broadcast against the N-D value then merged
+    to [M,N]; outputs returned as views of the group's shapes."""
+    rec = Recorder()
+    B, S, N, K = 2, 4, 16, 8
+    ops = (EpiOp("add", 0), EpiOp("add", 3), EpiOp("mul", 4), EpiOp("add", 5))
+    shape = (B, S, N)
+    spec = EpilogueSpec(1, 2, ops, BF, operand_shapes=((3, shape), (4, shape), (5, shape)),
+                        output_shapes=(shape,))
+    b = torch.randn(N, dtype=BF)
+    x, wt = torch.randn(B * S, K, dtype=BF), torch.randn(N, K, dtype=BF).t()
+    resid = torch.randn(B, S, N, dtype=BF)          # contiguous: merges to (N, 1)
+    per_batch = torch.randn(B, 1, N, dtype=BF)      # strides do not merge: materialised
+    row = torch.randn(1, 1, N, dtype=BF)            # broadcast row: (0, 1)
+    out = make(spec, 6, rec)(b, x, wt, resid, per_batch, row)
+    c = rec.calls[0]
+    assert (c["M"], c["N"], c["K"]) == (B * S, N, K)
+    assert c["operands"][0] == (0, 1, N, _abi.BF16)
+    assert c["operands"][1] == (N, 1, B * S * N, _abi.BF16)
+    assert c["operands"][2] == (N, 1, B * S * N, _abi.BF16)
+    assert c["operands"][3] == (0, 1, N, _abi.BF16)
+    assert out.shape == shape and out.is_contiguous()
