@@ -362,8 +362,8 @@ __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, 
 
 // SCHED selects the K-loop schedule: 0 lock-step waves, 1 ping-pong (8 waves,
 // two per SIMD), 3 one wave per SIMD (4 waves, 128x128 wave tiles, accumulators
-// in AGPRs) with two deep stages (BK=64) and the barrier before each stage's
-// last k-step.
+// in AGPRs) with two deep stages (BK=64), the barrier before each stage's last
+// k-step and each stage's DMA spread over three k-steps.
 template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T>
 __global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED == 3 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
@@ -472,6 +472,26 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // Stage `kt` of K into LDS slot `slot`.  A chunk whose k range starts at or
     // past K reads zeros (K is a multiple of 8, so a chunk is wholly inside or
     // wholly outside [0,K)).
+    // Chunks [c0, c1) of stage kt, A chunks first (0 .. A_DMA-1), then W chunks.
+    auto load_chunks = [&](int kt, int slot, auto c0, auto c1) {
+      const int k0 = kt * BK;
+      const uint32_t kb = (uint32_t)(k0 * 2);
+      char* st = smem + slot * STAGE;
+      static_for<decltype(c0)::value, decltype(c1)::value>([&](auto c) {
+        if constexpr (c < A_DMA) {
+          const uint32_t off = (k0 + a_k[c] < K) ? a_off[c] + kb : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              ra, (__attribute__((address_space(3))) void*)(st + (wave + NW * c) * G::kRowsPerDma * RB), 16,
+              off, 0, 0, 0);
+        } else {
+          constexpr int i = c - A_DMA;
+          const uint32_t off = (k0 + b_k[i] < K) ? b_off[i] + kb : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rb, (__attribute__((address_space(3))) void*)(st + A_BYTES + (wave + NW * i) * G::kRowsPerDma * RB),
+              16, off, 0, 0, 0);
+        }
+      });
+    };
     auto load_stage = [&](int kt, int slot) {
       const int k0 = kt * BK;
       const uint32_t kb = (uint32_t)(k0 * 2);
@@ -542,14 +562,25 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     if constexpr (SCHED == 3) {
       // One wave per SIMD, two stages of BK=64 (four MFMA k-steps each).  Stage k:
       //   k-steps 0..2: MFMAs of k-step s while k-step s+1's fragments are read;
+      //   under k-steps 0 and 1 the last two thirds of stage k+1's DMA are
+      //   issued (into stage k-1's slot, retired at barrier k-1);
       //   then this wave's LDS reads are complete and its DMA of stage k+1 has
-      //   landed, and the workgroup barrier: stage k+1 is visible, and no wave
-      //   reads stage k's slot any more (k-step 3's fragments are in registers);
-      //   k-step 3: MFMAs while the DMA of stage k+2 is issued into stage k's slot
-      //   and stage k+1's k-step 0 fragments are read.
-      // One barrier per 64 MFMAs per wave; the DMA has three k-steps plus one to
-      // land.
+      //   landed (nothing younger is in flight), and the workgroup barrier:
+      //   stage k+1 is visible, and no wave reads stage k's slot any more
+      //   (k-step 3's fragments are in registers);
+      //   k-step 3: MFMAs while the first third of stage k+2's DMA is issued
+      //   into stage k's slot and stage k+1's k-step 0 fragments are read.
+      // The stage's 64 KB of LDS writes are spread over three k-steps: written
+      // in one burst, they collide with the fragment reads (measured: writing
+      // them with ds_write instead of the DMA costs the same).  Past the last
+      // stage the DMA reads nothing (zero fill of a retired slot) and the
+      // fragments read are unused, so the loop body is straight-line code.
       static_assert(S == 2 && KS == 4, "two stages of four k-steps");
+      constexpr int P1 = (LPS + 2) / 3, P2 = (2 * LPS + 2) / 3;
+      using C0 = std::integral_constant<int, 0>;
+      using C1 = std::integral_constant<int, P1>;
+      using C2 = std::integral_constant<int, P2>;
+      using C3 = std::integral_constant<int, LPS>;
       i32x4_t fa[2][NI], fb[2][NJ];
       auto read = [&](const char* st, int ks, auto buf) {
         const int chunk = ((2 * ks + khalf) ^ swz) << 4;
@@ -578,36 +609,35 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       using Z = std::integral_constant<int, 0>;
       using O = std::integral_constant<int, 1>;
       using R = std::integral_constant<int, NI + NJ>;
-      using D = std::integral_constant<int, LPS>;
+      using D0 = std::integral_constant<int, P1>;
+      using D1 = std::integral_constant<int, P2 - P1>;
+      using D2 = std::integral_constant<int, LPS - P2>;
       load_stage(0, 0);
-      if (nk > 1) load_stage(1, 1);
-      if (nk > 1)
-        wait_vmcnt<LPS>();
-      else
-        wait_vmcnt<0>();
+      load_chunks(1, 1, C0{}, C1{});
+      wait_vmcnt<P1>();  // stage 0 (stage 1's first third may stay in flight)
       barrier();
       read(smem, 0, Z{});
       for (int k = 0; k < nk; ++k) {
         const char* st = smem + (k & 1) * STAGE;
+        char* nst = smem + ((k + 1) & 1) * STAGE;
         read(st, 1, O{});
+        load_chunks(k + 1, (k + 1) & 1, C1{}, C2{});
         mma(Z{});
-        interleave(R{}, Z{});
+        interleave(R{}, D1{});
         read(st, 2, Z{});
+        load_chunks(k + 1, (k + 1) & 1, C2{}, C3{});
         mma(O{});
-        interleave(R{}, Z{});
+        interleave(R{}, D2{});
         read(st, 3, O{});
         mma(Z{});
         interleave(R{}, Z{});
         wait_lgkmcnt0();
-        if (k + 1 < nk) wait_vmcnt<0>();  // this wave's DMA of stage k+1 (stage k+2 is not issued yet)
+        wait_vmcnt<0>();  // this wave's DMA of stage k+1 (stage k+2 is not issued yet)
         barrier();
-        // Straight-line code, so the DMA and reads interleave with the MFMAs: past
-        // the last stage the DMA reads nothing (zero fill of a slot that is not
-        // read again) and the fragments read are unused.
-        load_stage(k + 2, k & 1);
-        read(smem + ((k + 1) & 1) * STAGE, 0, Z{});
+        load_chunks(k + 2, k & 1, C0{}, C1{});
+        read(nst, 0, Z{});
         mma(O{});
-        interleave(R{}, D{});
+        interleave(R{}, D0{});
       }
     } else if constexpr (SCHED == 1) {
       // Ping-pong: waves 0-3 and 4-7 (one of each per SIMD) alternate between a
