@@ -339,19 +339,39 @@ __device__ __forceinline__ void gelu_tanh_n(float* v) {
   static_for<0, G>([&](auto e) { v[e] = v[e] * u[e]; });
 }
 
-// Byte address of 8-byte unit u (four 16-bit elements) of row r in an LDS
-// staging tile with BN columns.  Units are XOR-swizzled by (r & 31), so the 32
-// rows that one ds_read_b64/ds_write_b64 of the accumulator layout touches land
-// in 32 distinct bank pairs, and the two units of an aligned 16-byte chunk stay
-// together (swapped when r is odd).
+// LDS staging tile of BN 16-bit columns per row.  The 32 rows that one
+// ds_read_b64/ds_write_b64 of the accumulator layout touches must land in 32
+// distinct bank pairs, and a whole-row pass of 16-byte chunk accesses must not
+// conflict either.
+//  * BN >= 256 (32 or more chunks per row): chunk c of row r sits at chunk
+//    c ^ (r & 31).  Chunks stay whole, so the tile can be filled by the LDS DMA.
+//  * BN = 128 (16 chunks): 8-byte units are XOR-swizzled by (r & 31) instead,
+//    which swaps the two halves of a chunk on odd rows.
+template <int BN>
+constexpr bool kChunkSwizzle = BN >= 256;
+
+// Byte address of 8-byte unit u (four 16-bit elements) of row r.
 template <int BN>
 __device__ __forceinline__ int stage_unit(int r, int u) {
-  return r * (2 * BN) + ((u ^ (r & 31)) << 3);
+  if constexpr (kChunkSwizzle<BN>)
+    return r * (2 * BN) + ((((u >> 1) ^ (r & 31)) << 4) | ((u & 1) << 3));
+  else
+    return r * (2 * BN) + ((u ^ (r & 31)) << 3);
+}
+
+// Byte address of 16-byte chunk c of row r; read or written whole, its halves
+// are swapped when stage_swapped(r).
+template <int BN>
+__device__ __forceinline__ int stage_chunk(int r, int c) {
+  if constexpr (kChunkSwizzle<BN>)
+    return r * (2 * BN) + ((c ^ (r & 31)) << 4);
+  else
+    return r * (2 * BN) + (((2 * c) ^ (r & 31)) & ~1) * 8;
 }
 
 template <int BN>
-__device__ __forceinline__ int stage_chunk(int r, int c) {  // 16-byte chunk c of row r
-  return r * (2 * BN) + (((2 * c) ^ (r & 31)) & ~1) * 8;
+__device__ __forceinline__ bool stage_swapped(int r) {
+  return !kChunkSwizzle<BN> && (r & 1);
 }
 
 __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, x.w, x.x, x.y}; }
@@ -447,6 +467,70 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       });
     }
 
+    // The epilogue stages the first LDS-eligible 2-D operand of the chain in an
+    // LDS tile [BM][BN] of 16-bit elements that reuses the pipeline's slots.
+    int staged = -1;
+    for (int o = 0; o < d.n_ops; ++o) {
+      const int k = d.ops[o].kind;
+      if ((k == FUSEML_OP_ADD || k == FUSEML_OP_MUL) && (d.operands[d.ops[o].operand].reserved & kFlagStage)) {
+        staged = d.ops[o].operand;
+        break;
+      }
+    }
+    // With whole-chunk staging (BN >= 256) and a pipelined K loop the tile is
+    // filled by the LDS DMA.  Pipeline slot s holds staging rows [s*RPS,
+    // (s+1)*RPS), and a DMA of that slot's share of the operand goes to the
+    // same LDS address as the stage DMA it replaces: once no further stage of K
+    // is bound for a slot, the K loop's DMA issue points fetch the operand
+    // instead (same count per wave, so the vmcnt bookkeeping is unchanged), and
+    // the slot that holds the last stage is fetched after the loop.  Lane l of
+    // a DMA writes physical chunk l % CPR of row l / CPR and fetches the logical
+    // chunk that the staging swizzle places there.  A slot's DMAs go through a
+    // buffer resource whose base is the slot's first operand row, so the lane
+    // offsets do not depend on the slot.  Rows past M are not masked: they read
+    // in-bounds operand data (the resource's range check) that no result uses.
+    constexpr int SP = 2 * BN;        // staging row pitch in bytes
+    constexpr int CPR = BN / 8;       // 16-byte chunks per staged row
+    constexpr bool kOpDma = kChunkSwizzle<BN> && SCHED != 0;
+    constexpr int RPD = 1024 / SP;    // staging rows one wave-wide DMA fills
+    constexpr int RPS = STAGE / SP;   // staging rows per pipeline slot
+    static_assert(!kOpDma || (STAGE % SP == 0 && RPS % 32 == 0 && RPS == RPD * NW * LPS),
+                  "operand DMAs line up with the stage DMAs");
+    const bool op_dma = kOpDma && staged >= 0;
+    const void* op_ptr = d.a;
+    uint32_t op_bytes = a_bytes;
+    uint32_t op_o[kOpDma ? LPS : 1];  // chunk c's byte offset in its slot (kOOB: column past N)
+    uint64_t op_row_bytes = 0;        // operand row pitch in bytes
+    if constexpr (kOpDma) {
+      const int si = staged >= 0 ? staged : 0;
+      op_ptr = d.operands[si].ptr;
+      op_bytes = (uint32_t)(d.operands[si].extent * 2);
+      const uint32_t osm = (uint32_t)d.operands[si].stride_m;
+      op_row_bytes = (uint64_t)osm * 2u;
+      static_for<0, LPS>([&](auto c) {
+        const int r = (wave + NW * c) * RPD + lane / CPR;
+        const int n = n0 + 8 * ((lane % CPR) ^ (r & 31));
+        op_o[c] = n < N ? ((uint32_t)(m0 + r) * osm + (uint32_t)n) * 2u : kOOB;
+      });
+    }
+    // Base and byte extent of slot `slot`'s part of the operand.
+    auto op_slot_ptr = [&](int slot) -> const void* {
+      return static_cast<const char*>(op_ptr) + (uint64_t)(slot * RPS) * op_row_bytes;
+    };
+    auto op_slot_bytes = [&](int slot) -> uint32_t {
+      const uint64_t skip = (uint64_t)(slot * RPS) * op_row_bytes;
+      return skip < op_bytes ? op_bytes - (uint32_t)skip : 0u;
+    };
+    // Operand chunks [c0, c1) of slot `slot`.
+    auto load_op_chunks = [&](int slot, auto c0, auto c1) {
+      const __amdgpu_buffer_rsrc_t rop = make_rsrc(op_slot_ptr(slot), op_slot_bytes(slot));
+      char* st = smem + slot * STAGE;
+      static_for<decltype(c0)::value, decltype(c1)::value>([&](auto c) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rop, (__attribute__((address_space(3))) void*)(st + (wave + NW * c) * 1024), 16, op_o[c], 0, 0, 0);
+      });
+    };
+
     // Global -> LDS DMA.  One wave-wide buffer_load_dwordx4 ... lds writes 64 x 16
     // bytes contiguously from the LDS base in M0, i.e. kRowsPerDma whole stage
     // rows.  The swizzle is applied on the source side: the lane whose 16-byte
@@ -473,23 +557,27 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // past K reads zeros (K is a multiple of 8, so a chunk is wholly inside or
     // wholly outside [0,K)).
     // Chunks [c0, c1) of stage kt, A chunks first (0 .. A_DMA-1), then W chunks.
+    // Chunk c of either kind fills the 1 KB at (wave + NW*c) KB of the slot, as
+    // does the operand's chunk c (load_op_chunks).
+    static_assert(G::kRowsPerDma * RB == 1024 && A_BYTES == A_DMA * NW * 1024, "1 KB DMA blocks");
+    const int nk = (K + BK - 1) / BK;
     auto load_chunks = [&](int kt, int slot, auto c0, auto c1) {
       const int k0 = kt * BK;
       const uint32_t kb = (uint32_t)(k0 * 2);
       char* st = smem + slot * STAGE;
       static_for<decltype(c0)::value, decltype(c1)::value>([&](auto c) {
+        uint32_t off;
+        __amdgpu_buffer_rsrc_t r;
         if constexpr (c < A_DMA) {
-          const uint32_t off = (k0 + a_k[c] < K) ? a_off[c] + kb : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              ra, (__attribute__((address_space(3))) void*)(st + (wave + NW * c) * G::kRowsPerDma * RB), 16,
-              off, 0, 0, 0);
+          off = (k0 + a_k[c] < K) ? a_off[c] + kb : kOOB;
+          r = ra;
         } else {
           constexpr int i = c - A_DMA;
-          const uint32_t off = (k0 + b_k[i] < K) ? b_off[i] + kb : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rb, (__attribute__((address_space(3))) void*)(st + A_BYTES + (wave + NW * i) * G::kRowsPerDma * RB),
-              16, off, 0, 0, 0);
+          off = (k0 + b_k[i] < K) ? b_off[i] + kb : kOOB;
+          r = rb;
         }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r, (__attribute__((address_space(3))) void*)(st + (wave + NW * c) * 1024), 16, off, 0, 0, 0);
       });
     };
     auto load_stage = [&](int kt, int slot) {
@@ -548,7 +636,6 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       });
     };
 
-    const int nk = (K + BK - 1) / BK;
     // Workgroup barrier that keeps the compiler from moving any instruction
     // (MFMAs included) across it.  A bare s_barrier: __syncthreads() would add a
     // release fence that drains every in-flight DMA.
@@ -612,20 +699,28 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       using D0 = std::integral_constant<int, P1>;
       using D1 = std::integral_constant<int, P2 - P1>;
       using D2 = std::integral_constant<int, LPS - P2>;
-      load_stage(0, 0);
-      load_chunks(1, 1, C0{}, C1{});
-      wait_vmcnt<P1>();  // stage 0 (stage 1's first third may stay in flight)
-      barrier();
-      read(smem, 0, Z{});
-      for (int k = 0; k < nk; ++k) {
+      // Chunks [c0, c1) of stage kt into `slot`.  In the tail iterations (the
+      // last two), a stage kt >= nk is replaced by the operand's chunks of that
+      // slot when op_dma is set.  The steady-state body has no such branch: a
+      // branch, or a per-DMA select, there defeats the interleave hints.
+      auto issue = [&](int kt, int slot, auto c0, auto c1, auto tail) {
+        if constexpr (decltype(tail)::value) {
+          if (op_dma && kt >= nk) {
+            load_op_chunks(slot, c0, c1);
+            return;
+          }
+        }
+        load_chunks(kt, slot, c0, c1);
+      };
+      auto body = [&](int k, auto tail) {
         const char* st = smem + (k & 1) * STAGE;
         char* nst = smem + ((k + 1) & 1) * STAGE;
         read(st, 1, O{});
-        load_chunks(k + 1, (k + 1) & 1, C1{}, C2{});
+        issue(k + 1, (k + 1) & 1, C1{}, C2{}, tail);
         mma(Z{});
         interleave(R{}, D1{});
         read(st, 2, Z{});
-        load_chunks(k + 1, (k + 1) & 1, C2{}, C3{});
+        issue(k + 1, (k + 1) & 1, C2{}, C3{}, tail);
         mma(O{});
         interleave(R{}, D2{});
         read(st, 3, O{});
@@ -634,11 +729,24 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         wait_lgkmcnt0();
         wait_vmcnt<0>();  // this wave's DMA of stage k+1 (stage k+2 is not issued yet)
         barrier();
-        load_chunks(k + 2, k & 1, C0{}, C1{});
+        issue(k + 2, k & 1, C0{}, C1{}, tail);
         read(nst, 0, Z{});
         mma(O{});
         interleave(R{}, D0{});
-      }
+      };
+      using Tail = std::true_type;
+      issue(0, 0, C0{}, C3{}, Tail{});
+      issue(1, 1, C0{}, C1{}, Tail{});
+      wait_vmcnt<P1>();  // stage 0 (stage 1's first third may stay in flight)
+      barrier();
+      read(smem, 0, Z{});
+      const int steady = op_dma ? nk - 2 : nk;
+      int k = 0;
+      for (; k < steady; ++k) body(k, std::false_type{});
+      for (; k < nk; ++k) body(k, Tail{});
+      // The operand's remaining chunks: those of the slot that held the last
+      // stage (virtual stage nk+1, whose first third the last iteration issued).
+      if (op_dma) load_op_chunks((nk + 1) & 1, C1{}, C3{});
     } else if constexpr (SCHED == 1) {
       // Ping-pong: waves 0-3 and 4-7 (one of each per SIMD) alternate between a
       // memory phase (wait for the stage's DMA, read all its fragments into
@@ -651,10 +759,17 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       static_assert(NW == 8 && KS == 2, "ping-pong pairs two groups of four waves");
       const int grp = wave >> 2;
       i32x4_t fr_a[KS][NI], fr_b[KS][NJ];
+      using CL = std::integral_constant<int, LPS>;
+      using C0 = std::integral_constant<int, 0>;
+      // Slot p of a stage p >= nk, or of stage k+S-1 >= nk in memory phase k,
+      // takes its share of the operand (slot nk+S-1 (mod S) after the loop).
       static_for<0, S - 1>([&](auto p) {
-        if (p < nk) load_stage(p, p);
+        if (p < nk)
+          load_stage(p, p);
+        else if (op_dma)
+          load_op_chunks(p, C0{}, CL{});
       });
-      int issued = min(nk, S - 1);
+      int issued = op_dma ? S - 1 : min(nk, S - 1);  // stages (real or operand) issued
       auto mem = [&](int k) {
         const char* st = smem + (k % S) * STAGE;
         static_for<0, KS>([&](auto ks) {
@@ -666,8 +781,11 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
             fr_b[ks][j] = *reinterpret_cast<const i32x4_t*>(st + fb_row + 32 * j * RB + chunk);
           });
         });
-        if (k + S - 1 < nk) load_stage(k + S - 1, (k + S - 1) % S);
-        issued = min(nk, k + S);
+        if (k + S - 1 < nk)
+          load_stage(k + S - 1, (k + S - 1) % S);
+        else if (op_dma)
+          load_op_chunks((k + S - 1) % S, C0{}, CL{});
+        issued = op_dma ? k + S : min(nk, k + S);
         wait_lgkmcnt0();
       };
       auto comp = [&]() {
@@ -712,6 +830,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           end_phase(k + 1);
         }
       }
+      if (op_dma) load_op_chunks((nk + S - 1) % S, C0{}, CL{});
     } else {
       // S-stage pipeline: stages kt+1 .. kt+S-2 stay in flight while stage kt is
       // consumed; one barrier per stage both publishes the DMA of stage kt (after
@@ -753,7 +872,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         if (slot == q) aux[q * AUXLEN + tid] = elem_to_f32(aux_bits[q], dt);
       });
     }
-    __syncthreads();  // the epilogue reuses the stage LDS; the vector slots are written
+    if (op_dma) wait_vmcnt<0>();  // this wave's operand DMAs have landed
+    __syncthreads();  // the epilogue reuses the stage LDS; vector slots (and DMA-staged operand) written
 
     // ---------------------------------------------------------------------
     // Epilogue.  In accumulator block (i,j), register r of this lane holds
@@ -763,8 +883,6 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // operands and the output go through an LDS staging tile [BM][BN] of 16-bit
     // elements, filled and drained by whole-row coalesced 16-byte accesses.
     // ---------------------------------------------------------------------
-    constexpr int SP = 2 * BN;        // staging row pitch in bytes
-    constexpr int CPR = BN / 8;       // 16-byte chunks per staged row
     constexpr int RPP = NT / CPR;     // staged rows per cooperative pass
     static_assert(BM % RPP == 0 && BN % 128 == 0, "staging passes");
     static_assert(BM * SP <= S * STAGE, "staging tile fits in the pipeline's LDS");
@@ -777,18 +895,10 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     const int crow = tid / CPR;  // cooperative-pass row and chunk of this thread
     const int cchk = tid % CPR;
 
-    // (1) Stage the epilogue operands in LDS: the first LDS-eligible 2-D operand
-    // of the chain (all its global loads in flight together, one barrier).  The
-    // vector operands were written to their slots before the barrier above.
-    int staged = -1;
-    for (int o = 0; o < d.n_ops; ++o) {
-      const int k = d.ops[o].kind;
-      if ((k == FUSEML_OP_ADD || k == FUSEML_OP_MUL) && (d.operands[d.ops[o].operand].reserved & kFlagStage)) {
-        staged = d.ops[o].operand;
-        break;
-      }
-    }
-    if (staged >= 0) {
+    // (1) The staged operand, unless the DMA fetched it during the K loop: all
+    // its global loads in flight together, one barrier.  The vector operands
+    // were written to their slots before the barrier above.
+    if (staged >= 0 && !op_dma) {
       const void* optr = d.operands[staged].ptr;
       const int64_t osm = d.operands[staged].stride_m;
       const __amdgpu_buffer_rsrc_t r = make_rsrc(optr, (uint32_t)(d.operands[staged].extent * 2));
@@ -809,11 +919,11 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         });
         static_for<0, PB>([&](auto q) {
           const int rl = (b * PB + q) * RPP + crow;
-          *reinterpret_cast<i32x4_t*>(stg + stage_chunk<BN>(rl, cchk)) = (rl & 1) ? swap_halves(x[q]) : x[q];
+          *reinterpret_cast<i32x4_t*>(stg + stage_chunk<BN>(rl, cchk)) = stage_swapped<BN>(rl) ? swap_halves(x[q]) : x[q];
         });
       });
     }
-    if (staged >= 0) __syncthreads();
+    if (staged >= 0 && !op_dma) __syncthreads();
 
     // (2) The op chain, one column block at a time: for column block i, each op
     // runs over the NJ row blocks (NJ*16 independent elements) before the next
@@ -1014,7 +1124,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       });
       if (col_red) {
         // Column partials: reduce over the 32 rows held by each half-wave.  Column
-        // reductions never use the staged output, so LDS is free here.
+        // reductions use neither a staged output nor a staged operand (the host
+        // does not flag them), so the staging tile's LDS is free here.
         static_for<0, 16>([&](auto r) {
   #pragma unroll
           for (int sh = 1; sh < 32; sh <<= 1) {
@@ -1041,7 +1152,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         const int rl = p * RPP + crow;
         const int m = m0 + rl, n = n0 + 8 * cchk;
         i32x4_t x = *reinterpret_cast<const i32x4_t*>(stg + stage_chunk<BN>(rl, cchk));
-        if (rl & 1) x = swap_halves(x);
+        if (stage_swapped<BN>(rl)) x = swap_halves(x);
         if (m < M && n < N) {
           uint16_t* dst = reinterpret_cast<uint16_t*>(d.out.ptr) + (int64_t)m * d.out.ld + n;
           *reinterpret_cast<i32x4_t*>(dst) = x;
@@ -1051,7 +1162,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
 
     if (d.reduce_mask == 0) return;
     if (row_red) {
-      if (use_stage_out) __syncthreads();  // LDS staging tile is being drained
+      // The partials overwrite the staging tile, which other waves may still be
+      // draining (staged output) or reading (staged operand).
+      if (use_stage_out || staged >= 0) __syncthreads();
       // Row partials: the other half-wave holds the other 4-column runs of the same rows.
       static_for<0, NJ>([&](auto j) {
         const float s2 = rs[j] + __shfl_xor(rs[j], 32);
@@ -1257,8 +1370,11 @@ void derive_flags(fuseml_gemm_desc& d) {
     const int eb = op.dtype == FUSEML_F32 ? 4 : 2;
     const bool vec = op.stride_n == 1 && (op.stride_m % 4 == 0) && (d.N % 4 == 0) &&
                      ((uintptr_t)op.ptr % (4 * eb) == 0);
+    // Column reductions write their partials over the staging tile while other
+    // waves are still in the op chain, so they rule out a staged operand.
     const bool stage = eb == 2 && op.stride_n == 1 && op.stride_m != 0 && (op.stride_m % 8 == 0) &&
-                       (d.N % 8 == 0) && ((uintptr_t)op.ptr % 16 == 0);
+                       (d.N % 8 == 0) && ((uintptr_t)op.ptr % 16 == 0) &&
+                       !(d.reduce_mask != 0 && d.reduce_axis == 0);
     op.reserved = (vec ? kFlagVec4 : 0) | (stage ? kFlagStage : 0);
   }
   // Vector operands of ADD/MUL ops get LDS slots, in first-use order.

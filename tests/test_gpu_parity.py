@@ -221,6 +221,59 @@ def test_variant_reductions_parity(forced_variant, axis):
     _check_red(mean, ref["mean"], np.abs(v).mean(axis=axis), "mean")
 
 
+@pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
+@pytest.mark.parametrize("axis", [1, 0])
+@pytest.mark.parametrize("store_tile", [True, False], ids=["tile", "notile"])
+@pytest.mark.parametrize("shape", [(600, 1024, 200), (257, 512, 72)], ids=lambda s: "x".join(map(str, s)))
+def test_variant_reductions_with_tile_operand(forced_variant, axis, store_tile, shape):
+    """Reductions after a 2-D (LDS-staged) residual: the reduction partials reuse
+    the staging tile's LDS, with and without a staged output."""
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=25)
+    bias = (torch.rand(N, generator=_gen(26)) - 0.5).to(dtype)
+    resid = torch.randn(M, N, generator=_gen(27)).to(dtype)
+    inputs = [bias, resid, a, w.t()]
+    steps = [("add", 0, 1.0), ("add", 1, 1.0), ("sigmoid", -1, 1.0)]
+    outputs = ((("tile",),) if store_tile else ()) + (("red", "sum"), ("red", "amax"), ("red", "mean"))
+    spec = _spec(left=2, right=3, ops=steps, out_dtype=dtype, store_tile=store_tile,
+                 reductions=("sum", "amax", "mean"), reduce_axis=axis,
+                 reduce_dtypes=(torch.float32,) * 3, outputs=outputs)
+    print(f"case variant={forced_variant} reductions+tile operand axis={axis} "
+          f"store_tile={store_tile} shape={shape}", flush=True)
+    res = _launcher(spec, len(inputs))(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], 2, 3, steps, ("sum", "amax", "mean"), axis)
+    v = ref["tile"]
+    if store_tile:
+        _check_tile(res[0], v, f"{forced_variant} tile")
+        res = res[1:]
+    s, mx, mean = res
+    _check_red(s, ref["sum"], np.abs(v).sum(axis=axis), "sum")
+    _check_red(mx, ref["amax"], np.abs(v).max(axis=axis), "amax")
+    _check_red(mean, ref["mean"], np.abs(v).mean(axis=axis), "mean")
+
+
+@pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
+@pytest.mark.parametrize("K", [0, 8, 64, 96, 136])
+def test_variant_tile_operand_short_k(forced_variant, K):
+    """A 2-D operand with K of zero to a few stages: every way the staged
+    operand's LDS slots can be left free by a short K loop."""
+    M, N = 520, 776
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=28)
+    ops = _operands(M, N, dtype, seed=29)
+    inputs = ops + [a, w.t()]
+    left, right = len(ops), len(ops) + 1
+    steps = CHAINS["bias_residual"]
+    spec = _spec(left=left, right=right, ops=steps, out_dtype=dtype)
+    print(f"case variant={forced_variant} tile operand K={K}", flush=True)
+    out = _launcher(spec, len(inputs))(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], left, right, steps)["tile"]
+    _check_tile(out, ref, f"{forced_variant} K={K}")
+
+
 def test_escape_store_and_tile_with_reductions():
     """mm -> relu (escapes) -> row sum/amax/mean: the C4 group shape, small."""
     M, N, K = 320, 640, 256
