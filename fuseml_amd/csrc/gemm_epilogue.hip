@@ -130,6 +130,22 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Two values to packed 16-bit (a in the low half) with one v_cvt_pk_* each;
+// the same rounding (and fp16 saturation) as the scalar conversions above.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  a = fminf(fmaxf(a, -kFp16Max), kFp16Max);
+  b = fminf(fmaxf(b, -kFp16Max), kFp16Max);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+}
+
 __device__ __forceinline__ int dtype_bytes(int dtype) { return dtype == FUSEML_F32 ? 4 : 2; }
 
 // Load the 4 operand values at (m, n..n+3).  `ok` says the whole run of four is
@@ -188,18 +204,16 @@ __device__ __forceinline__ void store_out4(const Out& o, int m, int n, int M, in
     }
     return;
   }
-  uint32_t h[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    h[e] = (o.dtype == FUSEML_BF16) ? f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
+  uint2 w;
+  if (o.dtype == FUSEML_BF16)
+    w = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  else
+    w = make_uint2(pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3]));
   uint16_t* p = reinterpret_cast<uint16_t*>(o.ptr) + base;
   if (o.reserved & kFlagVec4) {
-    uint2 w;
-    w.x = h[0] | (h[1] << 16);
-    w.y = h[2] | (h[3] << 16);
     *reinterpret_cast<uint2*>(p) = w;
   } else {
-    for (int e = 0; e < 4 && n + e < N; ++e) p[e] = (uint16_t)h[e];
+    for (int e = 0; e < 4 && n + e < N; ++e) p[e] = (uint16_t)((e < 2 ? w.x : w.y) >> (16 * (e & 1)));
   }
 }
 
@@ -1086,15 +1100,25 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         if (use_stage_out) {
           const int r_loc = wm * TM + 32 * j + l32;
           const int u0 = (wn * TN + 32 * i) / 4 + khalf;
-          static_for<0, 4>([&](auto g) {
-            uint32_t h[4];
-            static_for<0, 4>([&](auto e) {
-              const float x = acc[i][j][4 * g + e];
-              h[e] = out_bf16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+          // One uniform branch per row block and one packed conversion per two
+          // values.  The arms end in different asm markers, so the compiler does
+          // not merge their LDS writes into one write of selected values (which
+          // the back end would split again into a branch per value).
+          if (out_bf16) {
+            static_for<0, 4>([&](auto g) {
+              const f32x16_t& v = acc[i][j];
+              *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
+                  make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
             });
-            *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
-                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-          });
+            asm volatile("; staged output, bf16");
+          } else {
+            static_for<0, 4>([&](auto g) {
+              const f32x16_t& v = acc[i][j];
+              *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
+                  make_uint2(pack_f16x2(v[4 * g], v[4 * g + 1]), pack_f16x2(v[4 * g + 2], v[4 * g + 3]));
+            });
+            asm volatile("; staged output, fp16");
+          }
         }
         if (d.out.ptr != nullptr && !use_stage_out) {
           static_for<0, 4>([&](auto g) {
@@ -1363,6 +1387,18 @@ int validate(const fuseml_gemm_desc* dp) {
   return FUSEML_OK;
 }
 
+// A chain that has no main output and ends in an escape store writes that
+// store as the main output: through the LDS staging tile as whole rows, not
+// from the accumulator layout (32 rows per store instruction).  The values and
+// the reductions after the chain are unchanged.
+void fold_final_store(fuseml_gemm_desc& d) {
+  if (d.out.ptr != nullptr || d.n_ops == 0) return;
+  const fuseml_epi_op& last = d.ops[d.n_ops - 1];
+  if (last.kind != FUSEML_OP_STORE) return;
+  d.out = d.extra[last.operand];
+  d.n_ops -= 1;
+}
+
 // Fill in the host-derived access-path flags (kept in the `reserved` fields).
 void derive_flags(fuseml_gemm_desc& d) {
   for (int i = 0; i < d.n_operands; ++i) {
@@ -1472,6 +1508,7 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
   }
 
   fuseml_gemm_desc d = *desc;
+  fold_final_store(d);
   derive_flags(d);
 
   if (d.reduce_mask) {
