@@ -946,6 +946,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // per column block.  Carrying one column block (not all of them) through the
     // runtime op loop keeps the loop's live values within the register file.
     const bool use_stage_out = d.out.ptr != nullptr && (d.out.reserved & kFlagStage) && !col_red;
+    // Activations run a step at a time across EW values (independent VALU
+    // chains).  16 instead of 8 for the one-wave schedule measured no faster.
+    constexpr int EW = 8;
     const bool out_bf16 = d.out.dtype == FUSEML_BF16;
     float rs[NJ], rmx[NJ];  // row partials (sum, max) of this lane's rows
     static_for<0, NJ>([&](auto j) {
@@ -955,6 +958,19 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     float* red_sum = reinterpret_cast<float*>(smem);
     float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
     static_for<0, NI>([&](auto i) {
+      // The column block enters the op loop in VGPRs.  In schedule 3 the
+      // accumulators live in AGPRs, and a value carried around the loop in an
+      // AGPR is copied out and back on every op (two extra VALU instructions per
+      // value per op, each a dependent pair).
+      if constexpr (SCHED == 3) {
+        static_for<0, NJ>([&](auto j) {
+          static_for<0, 16>([&](auto r) {
+            float x = acc[i][j][(int)r];
+            asm volatile("" : "+v"(x));
+            acc[i][j][(int)r] = x;
+          });
+        });
+      }
       for (int o = 0; o < d.n_ops; ++o) {
         // Lane coordinates through an opaque copy: the per-block addresses derived
         // from them are recomputed inside each op instead of being hoisted out of
@@ -1049,11 +1065,11 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
             break;
 #define FUSEML_EACH_N(fn)                                \
   static_for<0, NJ>([&](auto j) {                        \
-    static_for<0, 2>([&](auto h) {                       \
-      float x8[8];                                       \
-      static_for<0, 8>([&](auto e) { x8[e] = acc[i][j][8 * h + e]; }); \
-      fn<8>(x8);                                         \
-      static_for<0, 8>([&](auto e) { acc[i][j][8 * h + e] = x8[e]; }); \
+    static_for<0, 16 / EW>([&](auto h) {                 \
+      float xw[EW];                                      \
+      static_for<0, EW>([&](auto e) { xw[e] = acc[i][j][EW * h + e]; }); \
+      fn<EW>(xw);                                        \
+      static_for<0, EW>([&](auto e) { acc[i][j][EW * h + e] = xw[e]; }); \
     });                                                  \
   })
           case FUSEML_OP_GELU_ERF:
