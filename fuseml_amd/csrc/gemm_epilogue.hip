@@ -957,20 +957,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     });
     float* red_sum = reinterpret_cast<float*>(smem);
     float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
-    static_for<0, NI>([&](auto i) {
-      // The column block enters the op loop in VGPRs.  In schedule 3 the
-      // accumulators live in AGPRs, and a value carried around the loop in an
-      // AGPR is copied out and back on every op (two extra VALU instructions per
-      // value per op, each a dependent pair).
-      if constexpr (SCHED == 3) {
-        static_for<0, NJ>([&](auto j) {
-          static_for<0, 16>([&](auto r) {
-            float x = acc[i][j][(int)r];
-            asm volatile("" : "+v"(x));
-            acc[i][j][(int)r] = x;
-          });
-        });
-      }
+    // One column block: its NJ accumulator blocks A[j] through the op chain, then
+    // its stores, staged-output writes and reduction partials.
+    auto column_block = [&](f32x16_t(&A)[NJ], const int i) {
       for (int o = 0; o < d.n_ops; ++o) {
         // Lane coordinates through an opaque copy: the per-block addresses derived
         // from them are recomputed inside each op instead of being hoisted out of
@@ -1006,13 +995,13 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
                 x[4 * g + 2] = q.z;
                 x[4 * g + 3] = q.w;
               });
-              static_for<0, NJ>([&](auto j) { combine(acc[i][j], x); });
+              static_for<0, NJ>([&](auto j) { combine(A[j], x); });
             } else {  // column vector: one value per row
               static_for<0, NJ>([&](auto j) {
                 const float q = av[wm * TM + 32 * j + l32];
                 float x[16];
                 static_for<0, 16>([&](auto r) { x[r] = q; });
-                combine(acc[i][j], x);
+                combine(A[j], x);
               });
             }
           } else if (oi == staged) {
@@ -1028,7 +1017,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
                 x[4 * g + 2] = elem_to_f32(w.y & 0xffffu, dt);
                 x[4 * g + 3] = elem_to_f32(w.y >> 16, dt);
               });
-              combine(acc[i][j], x);
+              combine(A[j], x);
             });
           } else {
             static_for<0, NJ>([&](auto j) {
@@ -1038,7 +1027,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
                 const int n = nb + 8 * g;
                 load_operand4(d.operands[oi], m, n, m < M && n < N, x + 4 * g);
               });
-              combine(acc[i][j], x);
+              combine(A[j], x);
             });
           }
           continue;
@@ -1047,8 +1036,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           case FUSEML_OP_STORE:
             static_for<0, NJ>([&](auto j) {
               static_for<0, 4>([&](auto g) {
-                const float x[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                    acc[i][j][4 * g + 3]};
+                const float x[4] = {A[j][4 * g], A[j][4 * g + 1], A[j][4 * g + 2],
+                                    A[j][4 * g + 3]};
                 store_out4(d.extra[oi], mw + 32 * j, nb + 8 * g, M, N, x);
               });
             });
@@ -1056,8 +1045,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
 #define FUSEML_EACH(expr)                                \
   static_for<0, NJ>([&](auto j) {                        \
     static_for<0, 16>([&](auto r) {                      \
-      const float v = acc[i][j][(int)r];                 \
-      acc[i][j][(int)r] = (expr);                        \
+      const float v = A[j][(int)r];                 \
+      A[j][(int)r] = (expr);                        \
     });                                                  \
   })
           case FUSEML_OP_RELU:
@@ -1067,9 +1056,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   static_for<0, NJ>([&](auto j) {                        \
     static_for<0, 16 / EW>([&](auto h) {                 \
       float xw[EW];                                      \
-      static_for<0, EW>([&](auto e) { xw[e] = acc[i][j][EW * h + e]; }); \
+      static_for<0, EW>([&](auto e) { xw[e] = A[j][EW * h + e]; }); \
       fn<EW>(xw);                                        \
-      static_for<0, EW>([&](auto e) { acc[i][j][EW * h + e] = xw[e]; }); \
+      static_for<0, EW>([&](auto e) { A[j][EW * h + e] = xw[e]; }); \
     });                                                  \
   })
           case FUSEML_OP_GELU_ERF:
@@ -1122,14 +1111,14 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           // the back end would split again into a branch per value).
           if (out_bf16) {
             static_for<0, 4>([&](auto g) {
-              const f32x16_t& v = acc[i][j];
+              const f32x16_t& v = A[j];
               *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
                   make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
             });
             asm volatile("; staged output, bf16");
           } else {
             static_for<0, 4>([&](auto g) {
-              const f32x16_t& v = acc[i][j];
+              const f32x16_t& v = A[j];
               *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
                   make_uint2(pack_f16x2(v[4 * g], v[4 * g + 1]), pack_f16x2(v[4 * g + 2], v[4 * g + 3]));
             });
@@ -1138,8 +1127,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         }
         if (d.out.ptr != nullptr && !use_stage_out) {
           static_for<0, 4>([&](auto g) {
-            const float x[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                acc[i][j][4 * g + 3]};
+            const float x[4] = {A[j][4 * g], A[j][4 * g + 1], A[j][4 * g + 2],
+                                A[j][4 * g + 3]};
             store_out4(d.out, m, nb + 8 * g, M, N, x);
           });
         }
@@ -1150,7 +1139,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           static_for<0, 16>([&](auto r) {
             const int n = nb + 8 * (r >> 2) + (r & 3);
             const bool in = (m < M) && (n < N);
-            const float x = acc[i][j][(int)r];
+            const float x = A[j][(int)r];
             if (row_red && in) {
               rs[j] += x;
               rmx[j] = fmaxf(rmx[j], x);
@@ -1179,7 +1168,45 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           }
         });
       }
-    });
+    };
+    if constexpr (SCHED == 3) {
+      // A runtime loop over the column blocks, so that the op code exists once
+      // (not NI times: at NI = 4 the copies cost instruction-cache misses on
+      // every tile).  Each block is copied out of the AGPRs by a uniform branch
+      // (the asm markers keep the four copies from being merged into selects)
+      // and enters the op loop in VGPRs: a value carried around the op loop in
+      // an AGPR would be copied out and back on every op.
+#pragma clang loop unroll(disable)
+      for (int i = 0; i < NI; ++i) {
+        f32x16_t A[NJ];
+        static_for<0, NI>([&](auto ii) {
+          if (i == ii) {
+            static_for<0, NJ>([&](auto j) { A[j] = acc[ii][j]; });
+            asm volatile("; column block %0" ::"n"((int)ii));
+          }
+        });
+        static_for<0, NJ>([&](auto j) {
+          static_for<0, 16>([&](auto r) {
+            float x = A[j][(int)r];
+            asm volatile("" : "+v"(x));
+            A[j][(int)r] = x;
+          });
+        });
+        column_block(A, i);
+      }
+    } else {
+      // Also one copy of the op code: block i is processed in acc[0] and the
+      // later blocks are shifted down after it (acc lives in VGPRs here; copying
+      // a block out instead, as above, needs more registers than two waves per
+      // SIMD have).
+#pragma clang loop unroll(disable)
+      for (int i = 0; i < NI; ++i) {
+        column_block(acc[0], i);
+        static_for<0, NI - 1>([&](auto q) {
+          static_for<0, NJ>([&](auto j) { acc[q][j] = acc[q + 1][j]; });
+        });
+      }
+    }
 
     // (3) Staged output: the LDS tile (written above), drained by whole-row
     // 16-byte stores.
