@@ -397,7 +397,7 @@ __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, 
 // SCHED selects the K-loop schedule: 0 lock-step waves, 1 ping-pong (8 waves,
 // two per SIMD), 3 one wave per SIMD (4 waves, 128x128 wave tiles, accumulators
 // in AGPRs) with two deep stages (BK=64), the barrier before each stage's last
-// k-step and each stage's DMA spread over three k-steps.
+// k-step and each stage's DMA split over two k-steps.
 template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T>
 __global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED == 3 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
@@ -663,21 +663,23 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     if constexpr (SCHED == 3) {
       // One wave per SIMD, two stages of BK=64 (four MFMA k-steps each).  Stage k:
       //   k-steps 0..2: MFMAs of k-step s while k-step s+1's fragments are read;
-      //   under k-steps 0 and 1 the last two thirds of stage k+1's DMA are
-      //   issued (into stage k-1's slot, retired at barrier k-1);
+      //   under k-step 0 the second half of stage k+1's DMA is issued (into
+      //   stage k-1's slot, retired at barrier k-1);
       //   then this wave's LDS reads are complete and its DMA of stage k+1 has
       //   landed (nothing younger is in flight), and the workgroup barrier:
       //   stage k+1 is visible, and no wave reads stage k's slot any more
       //   (k-step 3's fragments are in registers);
-      //   k-step 3: MFMAs while the first third of stage k+2's DMA is issued
+      //   k-step 3: MFMAs while the first half of stage k+2's DMA is issued
       //   into stage k's slot and stage k+1's k-step 0 fragments are read.
-      // The stage's 64 KB of LDS writes are spread over three k-steps: written
-      // in one burst, they collide with the fragment reads (measured: writing
-      // them with ds_write instead of the DMA costs the same).  Past the last
-      // stage the DMA reads nothing (zero fill of a retired slot) and the
-      // fragments read are unused, so the loop body is straight-line code.
+      // The stage's 64 KB of LDS writes are split over two k-steps: written in
+      // one burst they collide with the fragment reads (measured: writing them
+      // with ds_write instead of the DMA costs the same), and issued later they
+      // have less time to land (measured: halves 2% faster than thirds over
+      // k-steps 3, 0 and 1).  Past the last stage the DMA reads nothing (zero
+      // fill of a retired slot) and the fragments read are unused, so the loop
+      // body is straight-line code.
       static_assert(S == 2 && KS == 4, "two stages of four k-steps");
-      constexpr int P1 = (LPS + 2) / 3, P2 = (2 * LPS + 2) / 3;
+      constexpr int P1 = LPS / 2, P2 = LPS;
       using C0 = std::integral_constant<int, 0>;
       using C1 = std::integral_constant<int, P1>;
       using C2 = std::integral_constant<int, P2>;
@@ -751,7 +753,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       using Tail = std::true_type;
       issue(0, 0, C0{}, C3{}, Tail{});
       issue(1, 1, C0{}, C1{}, Tail{});
-      wait_vmcnt<P1>();  // stage 0 (stage 1's first third may stay in flight)
+      wait_vmcnt<P1>();  // stage 0 (stage 1's first half may stay in flight)
       barrier();
       read(smem, 0, Z{});
       const int steady = op_dma ? nk - 2 : nk;
@@ -759,7 +761,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       for (; k < steady; ++k) body(k, std::false_type{});
       for (; k < nk; ++k) body(k, Tail{});
       // The operand's remaining chunks: those of the slot that held the last
-      // stage (virtual stage nk+1, whose first third the last iteration issued).
+      // stage (virtual stage nk+1, whose first half the last iteration issued).
       if (op_dma) load_op_chunks((nk + 1) & 1, C1{}, C3{});
     } else if constexpr (SCHED == 1) {
       // Ping-pong: waves 0-3 and 4-7 (one of each per SIMD) alternate between a
