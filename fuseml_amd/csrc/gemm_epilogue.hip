@@ -731,14 +731,20 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       auto body = [&](int k, auto tail) {
         const char* st = smem + (k & 1) * STAGE;
         char* nst = smem + ((k + 1) & 1) * STAGE;
+        // Each k-step is its own scheduling region (sched_barrier(0) between
+        // them): otherwise the scheduler pulls the next k-step's MFMAs forward,
+        // right behind those of the same accumulator and behind the reads of
+        // their fragments, and every MFMA waits on lgkmcnt(0).
         read(st, 1, O{});
         issue(k + 1, (k + 1) & 1, C1{}, C2{}, tail);
         mma(Z{});
         interleave(R{}, D1{});
+        __builtin_amdgcn_sched_barrier(0);
         read(st, 2, Z{});
         issue(k + 1, (k + 1) & 1, C2{}, C3{}, tail);
         mma(O{});
         interleave(R{}, D2{});
+        __builtin_amdgcn_sched_barrier(0);
         read(st, 3, O{});
         mma(Z{});
         interleave(R{}, Z{});
@@ -749,6 +755,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         read(nst, 0, Z{});
         mma(O{});
         interleave(R{}, D0{});
+        __builtin_amdgcn_sched_barrier(0);
       };
       using Tail = std::true_type;
       issue(0, 0, C0{}, C3{}, Tail{});
