@@ -793,7 +793,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           load_op_chunks(p, C0{}, CL{});
       });
       int issued = op_dma ? S - 1 : min(nk, S - 1);  // stages (real or operand) issued
-      auto mem = [&](int k) {
+      // Memory phase k.  `steady`: stage k+S-1 exists (k + S - 1 < nk), so the
+      // DMA needs no branch.
+      auto mem = [&](int k, auto steady) {
         const char* st = smem + (k % S) * STAGE;
         static_for<0, KS>([&](auto ks) {
           const int chunk = ((2 * ks + khalf) ^ swz) << 4;
@@ -804,11 +806,16 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
             fr_b[ks][j] = *reinterpret_cast<const i32x4_t*>(st + fb_row + 32 * j * RB + chunk);
           });
         });
-        if (k + S - 1 < nk)
+        if constexpr (decltype(steady)::value) {
           load_stage(k + S - 1, (k + S - 1) % S);
-        else if (op_dma)
-          load_op_chunks((k + S - 1) % S, C0{}, CL{});
-        issued = op_dma ? k + S : min(nk, k + S);
+          issued = k + S;
+        } else {
+          if (k + S - 1 < nk)
+            load_stage(k + S - 1, (k + S - 1) % S);
+          else if (op_dma)
+            load_op_chunks((k + S - 1) % S, C0{}, CL{});
+          issued = op_dma ? k + S : min(nk, k + S);
+        }
         wait_lgkmcnt0();
       };
       auto comp = [&]() {
@@ -820,13 +827,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       };
       // End of a phase: this wave's DMAs of stage `need` (read by the next
       // memory phase) have landed, then the workgroup barrier.
-      auto end_phase = [&](int need) {
-        if (need < nk) {
-          const int allowed = min(max(issued - need - 1, 0), S - 1);
-          static_for<0, S>([&](auto a) {
-            if (allowed == a) wait_vmcnt<LPS * a>();
-          });
-        }
+      auto phase_barrier = [&]() {
         // sched_barrier(0) keeps the scheduler from moving any instruction
         // (MFMAs included) across the phase boundary.
         __builtin_amdgcn_sched_barrier(0);
@@ -835,10 +836,40 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
       };
+      auto end_phase = [&](int need) {
+        if (need < nk) {
+          const int allowed = min(max(issued - need - 1, 0), S - 1);
+          static_for<0, S>([&](auto a) {
+            if (allowed == a) wait_vmcnt<LPS * a>();
+          });
+        }
+        phase_barrier();
+      };
+      // The same at a point where `allowed` is known at compile time (in the
+      // steady state the runtime choice above is a chain of branches per phase).
+      auto end_phase_c = [&](auto allowed) {
+        __builtin_amdgcn_sched_barrier(0);  // the wait stays behind the phase's work
+        wait_vmcnt<LPS * decltype(allowed)::value>();
+        phase_barrier();
+      };
+      // Memory phases 0 .. steady-1 issue a real stage; the rest run the
+      // general code.  In the steady state a memory phase k leaves the stages
+      // k+1 .. k+S-1 in flight after stage k: S-1 stages younger than the one
+      // group 0 needs next (stage k), S-2 younger than stage k+1.
+      const int steady = max(nk - (S - 1), 0);
+      using A1 = std::integral_constant<int, S - 1>;
+      using A2 = std::integral_constant<int, S - 2>;
       end_phase(0);    // stage 0 has landed before the first memory phase reads it
       if (grp == 0) {  // phases 2k: mem(k), 2k+1: comp(k), 2nk: idle
-        for (int k = 0; k < nk; ++k) {
-          mem(k);
+        int k = 0;
+        for (; k < steady; ++k) {
+          mem(k, std::true_type{});
+          end_phase_c(A1{});
+          comp();
+          end_phase_c(A2{});
+        }
+        for (; k < nk; ++k) {
+          mem(k, std::false_type{});
           end_phase(k);
           comp();
           end_phase(k + 1);
@@ -846,8 +877,15 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         end_phase(nk);
       } else {  // phase 0: idle, 2k+1: mem(k), 2k+2: comp(k)
         end_phase(0);
-        for (int k = 0; k < nk; ++k) {
-          mem(k);
+        int k = 0;
+        for (; k < steady; ++k) {
+          mem(k, std::true_type{});
+          end_phase_c(A2{});
+          comp();
+          end_phase_c(A2{});
+        }
+        for (; k < nk; ++k) {
+          mem(k, std::false_type{});
           end_phase(k + 1);
           comp();
           end_phase(k + 1);
