@@ -1259,9 +1259,10 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // 16-byte stores.
     if (use_stage_out) {
       __syncthreads();
-      // A short loop rather than BM/RPP unrolled passes: this code runs once per
-      // tile, and its size is paid in instruction-cache misses.
-#pragma unroll 4
+      // 16 passes unrolled: their LDS reads are in flight together (measured 2%
+      // faster than 4 at 16384x4096x1024 with no ops; the kernel's code is small
+      // enough since the column blocks share one copy of the op code).
+#pragma unroll 16
       for (int p = 0; p < BM / RPP; ++p) {
         const int rl = p * RPP + crow;
         const int m = m0 + rl, n = n0 + 8 * cchk;
