@@ -11,20 +11,26 @@
 // cuBLASLt epilogue extension (fuseml/codegen/cublas_epilogue.py:355-557).
 //
 // Kernel structure (per workgroup = one BM x BN output tile):
-//   * Both operands are K-contiguous in HBM (A = x[M,K]; B = t(W), i.e. W[N,K]),
-//     so both are staged into LDS as [rows][BK=64] bf16 rows of 128 bytes, with
-//     the 16-byte chunk index XOR-swizzled by (row & 7) so that the 32 lanes of a
-//     ds_read_b128 that read one chunk column of 32 consecutive rows hit 8
-//     distinct chunk slots per 8 rows (no bank conflicts).
-//   * Two LDS stages (double buffering): the global loads of K-tile t+1 are
-//     issued into registers before the MFMAs of tile t, and written to the
-//     other stage afterwards; one barrier per K-tile.
-//   * Global loads are raw buffer loads: an out-of-range offset returns zeros,
-//     which implements the M/N/K boundary masking with no branches.
+//   * Both operands are K-contiguous in HBM (A = x[M,K]; B = t(W), i.e. W[N,K]).
+//     A K-stage holds BK columns of the tile's A rows and W rows in LDS, rows of
+//     2*BK bytes with the 16-byte chunk index XOR-swizzled so that the MFMA
+//     fragment reads (ds_read_b128) are free of bank conflicts.
+//   * Stages are filled by the global -> LDS DMA (buffer_load_dwordx4 ... lds):
+//     no staging registers, and an out-of-range offset returns zeros, which masks
+//     the M/N/K edges with no branches.
+//   * Three K-loop schedules (template parameter SCHED), one per tile variant:
+//     256x256 ping-pong (8 waves, two groups alternating memory and compute
+//     phases, BK=32, 4 stages), 256x256 one wave per SIMD (4 waves, 128x128
+//     accumulators in AGPRs, BK=64, 2 stages), and 128x128 lock-step.
 //   * MFMA roles are swapped (MFMA "A" = rows of W, MFMA "B" = rows of x) so that
 //     each lane's accumulator holds one output row m and runs of 4 consecutive
-//     columns n: epilogue operands are read and the output is written as 8-byte
-//     vectors, and a row reduction needs a single cross-half-wave exchange.
+//     columns n; a row reduction needs a single cross-half-wave exchange.
+//   * Epilogue: the op chain from the kernel-argument descriptor, one column
+//     block at a time in a runtime loop (one copy of the op code).  Vector
+//     operands come from fp32 LDS slots, the first 2-D operand from an LDS
+//     staging tile (fetched by the DMA during the K loop's last stages in the
+//     256-wide variants), and the output is staged in LDS and stored as whole
+//     rows.
 //   * The workgroup -> tile map is XCD-aware: the hardware deals workgroups to
 //     the 8 XCDs round-robin, so each XCD is given a contiguous range of
 //     logical tiles, ordered in GROUP_M-row column strips for L2 reuse.
