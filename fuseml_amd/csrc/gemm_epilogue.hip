@@ -905,27 +905,37 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       static_for<0, S - 1>([&](auto p) {
         if (p < nk) load_stage(p, p);
       });
-      int slot = 0;
-      for (int kt = 0; kt < nk; ++kt) {
-        const int ahead = min(nk - 1 - kt, S - 2);  // stages issued after kt
-        if (ahead == S - 2) {
-          wait_vmcnt<LPS * (S - 2)>();
-        } else {
-          static_for<0, S - 2>([&](auto q) {
-            if (ahead == q) wait_vmcnt<LPS * q>();
-          });
-        }
-        // A bare s_barrier: __syncthreads() would add a release fence that drains
-        // every in-flight DMA.  The asm statements only stop the compiler from
-        // moving memory accesses across the barrier.
+      // A bare s_barrier: __syncthreads() would add a release fence that drains
+      // every in-flight DMA.  The asm statements only stop the compiler from
+      // moving memory accesses across the barrier.
+      auto stage_barrier = [&]() {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kt + S - 1 < nk) {
-          int nslot = slot + S - 1;
-          if (nslot >= S) nslot -= S;
-          load_stage(kt + S - 1, nslot);
-        }
+      };
+      int slot = 0;
+      auto next_slot = [&]() {
+        int nslot = slot + S - 1;
+        return nslot >= S ? nslot - S : nslot;
+      };
+      // While stage kt+S-1 exists, S-2 stages are in flight after kt and the
+      // refill needs no branch; the last S-1 stages run the general code.
+      const int steady = max(nk - (S - 1), 0);
+      int kt = 0;
+      for (; kt < steady; ++kt) {
+        wait_vmcnt<LPS * (S - 2)>();
+        stage_barrier();
+        load_stage(kt + S - 1, next_slot());
+        compute(smem + slot * STAGE);
+        if (++slot == S) slot = 0;
+      }
+      for (; kt < nk; ++kt) {
+        const int ahead = min(nk - 1 - kt, S - 2);  // stages issued after kt
+        static_for<0, S - 1>([&](auto q) {
+          if (ahead == q) wait_vmcnt<LPS * q>();
+        });
+        stage_barrier();
+        if (kt + S - 1 < nk) load_stage(kt + S - 1, next_slot());
         compute(smem + slot * STAGE);
         if (++slot == S) slot = 0;
       }
