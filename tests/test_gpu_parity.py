@@ -274,6 +274,29 @@ def test_variant_tile_operand_short_k(forced_variant, K):
     _check_tile(out, ref, f"{forced_variant} K={K}")
 
 
+@pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
+@pytest.mark.parametrize("shape", [(600, 1024, 200), (257, 512, 72)], ids=lambda s: "x".join(map(str, s)))
+def test_variant_fp16_chain(forced_variant, shape):
+    """fp16 GEMM operands (f16 MFMA), an fp16 residual through the staging tile
+    and an fp16 staged output, saturated at +-65504, on every variant."""
+    M, N, K = shape
+    dtype = torch.float16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=31)
+    bias = (torch.rand(N, generator=_gen(32)) - 0.5).to(dtype)
+    resid = torch.randn(M, N, generator=_gen(33)).to(dtype)
+    inputs = [bias, resid, a, w.t()]
+    steps = [("add", 0, 1.0), ("gelu_erf", -1, 1.0), ("add", 1, 1.0), ("scale", -1, 3.0e4)]
+    spec = _spec(left=2, right=3, ops=steps, out_dtype=dtype)
+    print(f"case variant={forced_variant} fp16 chain shape={shape}", flush=True)
+    out = _launcher(spec, len(inputs))(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], 2, 3, steps)["tile"]
+    ref_sat = np.clip(ref, -ora.FP16_MAX, ora.FP16_MAX)
+    got = _np(out)
+    assert np.isfinite(got).all()
+    assert np.allclose(got, ref_sat, rtol=RTOL, atol=ATOL * 3.0e4)
+
+
 def test_escape_store_and_tile_with_reductions():
     """mm -> relu (escapes) -> row sum/amax/mean: the C4 group shape, small."""
     M, N, K = 320, 640, 256
