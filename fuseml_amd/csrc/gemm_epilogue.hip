@@ -754,6 +754,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         read(st, 3, O{});
         mma(Z{});
         interleave(R{}, Z{});
+        __builtin_amdgcn_sched_barrier(0);  // the waits stay behind k-step 2's MFMAs
         wait_lgkmcnt0();
         wait_vmcnt<0>();  // this wave's DMA of stage k+1 (stage k+2 is not issued yet)
         barrier();
