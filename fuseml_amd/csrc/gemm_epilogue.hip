@@ -10,7 +10,7 @@
 // epilogue emitters 1599-1903, store 1544-1593, reductions 1909-2018) and the
 // cuBLASLt epilogue extension (fuseml/codegen/cublas_epilogue.py:355-557).
 //
-// Kernel structure (per workgroup = one BM x BN output tile):
+// Kernel structure (per workgroup: one BM x BN output tile at a time):
 //   * Both operands are K-contiguous in HBM (A = x[M,K]; B = t(W), i.e. W[N,K]).
 //     A K-stage holds BK columns of the tile's A rows and W rows in LDS, rows of
 //     2*BK bytes with the 16-byte chunk index XOR-swizzled so that the MFMA
@@ -31,9 +31,11 @@
 //     staging tile (fetched by the DMA during the K loop's last stages in the
 //     256-wide variants), and the output is staged in LDS and stored as whole
 //     rows.
-//   * The workgroup -> tile map is XCD-aware: the hardware deals workgroups to
-//     the 8 XCDs round-robin, so each XCD is given a contiguous range of
-//     logical tiles, ordered in GROUP_M-row column strips for L2 reuse.
+//   * The 256-wide variants launch at most one workgroup per CU, each running
+//     tiles b, b + grid, ... in turn.  The tile map is XCD-aware: the hardware
+//     deals workgroups to the 8 XCDs round-robin, so each XCD is given a
+//     contiguous range of each round's logical tiles, ordered in GROUP_M-row
+//     column strips for L2 reuse.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -43,6 +45,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "fuseml_hip.h"
@@ -407,7 +410,6 @@ __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, 
 template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T>
 __global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED == 3 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
-  KDesc& d = *(KDesc*)(__builtin_amdgcn_kernarg_segment_ptr());
   using G = StageGeom<BK>;
   constexpr int NW = WM * WN;  // waves per workgroup
   constexpr int NT = NW * 64;
@@ -430,25 +432,49 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   __shared__ __attribute__((aligned(1024))) char smem[S * STAGE + kAuxSlots * AUXLEN * 4];
   float* aux = reinterpret_cast<float*>(smem + S * STAGE);
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN;
-  const int wn = wave % WN;
+  const KDesc& dk = *(const KDesc*)(__builtin_amdgcn_kernarg_segment_ptr());
+  const int tiles_m = ((int)dk.M + BM - 1) / BM;
+  const int tiles_n = ((int)dk.N + BN - 1) / BN;
 
-  const int M = (int)d.M, N = (int)d.N, K = (int)d.K;
-  const int tiles_m = (M + BM - 1) / BM;
-  const int tiles_n = (N + BN - 1) / BN;
-
-  // One workgroup per tile.  XCD-aware order: the hardware deals workgroups to
-  // the 8 XCDs round-robin (XCD = blockIdx % 8), so each XCD is given a
-  // contiguous range of logical tiles; consecutive logical tiles form
+  // Workgroup b runs tiles b, b + nwg, b + 2*nwg, ... (the 256-wide variants
+  // launch at most one workgroup per CU, so a workgroup runs several tiles
+  // back to back with no relaunch).  Round r is tiles [r*nwg, r*nwg + nwg).
+  // XCD-aware order within a round: the hardware deals workgroups to the 8
+  // XCDs round-robin (XCD = blockIdx % 8), so each XCD is given a contiguous
+  // range of the round's logical tiles; consecutive logical tiles form
   // GROUP_M-row column strips, so the tiles an XCD runs at the same time share
   // A rows and B columns in its L2.
   const int nwg = gridDim.x;
-  int lid = blockIdx.x;
-  if ((nwg & 7) == 0) lid = (lid & 7) * (nwg >> 3) + (lid >> 3);
-  {
+  const int ntiles = tiles_m * tiles_n;
+  for (int tile = blockIdx.x; tile < ntiles; tile += nwg) {
+    const int round0 = tile - (int)blockIdx.x;
+    const int in_round = min(nwg, ntiles - round0);
+    int lid = tile;
+    if ((in_round & 7) == 0) lid = round0 + ((int)blockIdx.x & 7) * (in_round >> 3) + ((int)blockIdx.x >> 3);
+    if (tile != (int)blockIdx.x) {
+      // The previous tile's LDS reads and global stores are complete in every
+      // wave before this tile's DMA overwrites the slots.
+      __builtin_amdgcn_sched_barrier(0);
+      wait_lgkmcnt0();
+      wait_vmcnt<0>();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // The descriptor pointer and the thread index pass through empty asm each
+    // tile, so nothing derived from them is hoisted out of the tile loop: held
+    // across the K loop, the epilogue's address arithmetic would spill.
+    const char* kargs = (const char*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kargs));
+    const KDesc& d = *(const KDesc*)kargs;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+    const int M = (int)d.M, N = (int)d.N, K = (int)d.K;
     const int strip = kGroupM * tiles_n;
     const int first_m = (lid / strip) * kGroupM;
     const int strip_h = min(tiles_m - first_m, kGroupM);
@@ -1276,7 +1302,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       }
     }
 
-    if (d.reduce_mask == 0) return;
+    if (d.reduce_mask == 0) continue;
     if (row_red) {
       // The partials overwrite the staging tile, which other waves may still be
       // draining (staged output) or reading (staged operand).
@@ -1311,7 +1337,6 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       if (d.reduce_mask & FUSEML_RED_AMAX) atomic_max_f32(d.reduce_out[1] + idx, mx);
       if (d.reduce_mask & FUSEML_RED_MEAN) atomicAdd(d.reduce_out[2] + idx, s * inv);
     }
-
   }
 }
 
@@ -1526,9 +1551,12 @@ void derive_flags(fuseml_gemm_desc& d) {
   for (int i = 0; i < d.n_extra; ++i) out_flags(d.extra[i]);
 }
 
+// `max_wg` caps the grid (0: one workgroup per tile); the kernel loops over the
+// remaining tiles.
 template <const TileConfig& C>
-hipError_t launch_variant(const fuseml_gemm_desc& d, hipStream_t stream) {
-  const int64_t tiles = cdiv(d.M, C.bm) * cdiv(d.N, C.bn);
+hipError_t launch_variant(const fuseml_gemm_desc& d, hipStream_t stream, int max_wg) {
+  int64_t tiles = cdiv(d.M, C.bm) * cdiv(d.N, C.bn);
+  if (max_wg > 0 && tiles > max_wg) tiles = max_wg;
   const dim3 grid((unsigned)tiles), block(C.wm * C.wn * 64);
   if (d.ab_dtype == FUSEML_BF16)
     hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16>), grid,
@@ -1580,6 +1608,40 @@ int fuseml_device_arch(int device, char* buf, int buflen) {
   return FUSEML_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Per-device check and CU count, queried once per device: the CU count for a
+// gfx950 device, else FUSEML_EDEVICE or FUSEML_EHIP (negative; the error is set).
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_device_cus[kMaxDevices];
+
+int device_cus(int dev) {
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int known = g_device_cus[dev].load(std::memory_order_relaxed);
+    if (known > 0) return known;
+  }
+  char arch[64];
+  if (fuseml_device_arch(dev, arch, sizeof(arch)) != FUSEML_OK) return FUSEML_EHIP;
+  if (strncmp(arch, "gfx950", 6) != 0) {
+    set_error("device %d is %s; kernels are built for gfx950 only", dev, arch);
+    return FUSEML_EDEVICE;
+  }
+  int cus = 0;
+  const hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess || cus <= 0) {
+    set_error("hipDeviceGetAttribute(MultiprocessorCount): %s", hipGetErrorString(e));
+    return FUSEML_EHIP;
+  }
+  if (dev >= 0 && dev < kMaxDevices) g_device_cus[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+}  // namespace
+
+extern "C" {
+
 int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
   g_last_error[0] = '\0';
   int rc = validate(desc);
@@ -1592,12 +1654,8 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
     set_error("hipGetDevice: %s", hipGetErrorString(e));
     return FUSEML_EHIP;
   }
-  char arch[64];
-  if (fuseml_device_arch(dev, arch, sizeof(arch)) != FUSEML_OK) return FUSEML_EHIP;
-  if (strncmp(arch, "gfx950", 6) != 0) {
-    set_error("device %d is %s; kernels are built for gfx950 only", dev, arch);
-    return FUSEML_EDEVICE;
-  }
+  const int cus = device_cus(dev);
+  if (cus <= 0) return cus < 0 ? cus : FUSEML_EHIP;
 
   fuseml_gemm_desc d = *desc;
   fold_final_store(d);
@@ -1619,11 +1677,11 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
 
   const TileConfig c = choose_config(d);
   if (c.sched == kDeep.sched)
-    e = launch_variant<kDeep>(d, stream);
+    e = launch_variant<kDeep>(d, stream, cus);
   else if (c.sched == kLarge.sched)
-    e = launch_variant<kLarge>(d, stream);
+    e = launch_variant<kLarge>(d, stream, cus);
   else
-    e = launch_variant<kSmall>(d, stream);
+    e = launch_variant<kSmall>(d, stream, 0);
   if (e != hipSuccess) {
     set_error("gemm_epilogue launch: %s", hipGetErrorString(e));
     return FUSEML_EHIP;
