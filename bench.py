@@ -131,33 +131,20 @@ def _initial_state(name, wl):
 TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "traffic_{workload}.md")
 
 
-def _grid_of(launcher, M, N):
-    import ctypes
-
-    from fuseml_amd import _abi
-
-    d = _abi.GemmDesc()
-    d.M, d.N, d.K = M, N, 64
-    d.a, d.lda, d.b, d.ldb = 16, 64, 16, 64
-    d.ab_dtype = _abi.BF16
-    d.out.ptr, d.out.ld, d.out.dtype = 16, N, _abi.BF16
-    cfg = (ctypes.c_int32 * 4)()
-    if launcher._lib.fuseml_gemm_epilogue_config(ctypes.byref(d), cfg) != 0:
-        return None
-    return ((M + cfg[0] - 1) // cfg[0]) * ((N + cfg[1] - 1) // cfg[1]) * cfg[2] * 64
-
-
-def _traffic(workload, grid_threads):
-    """Bytes per launch for the kernel with this grid (threads), or None."""
+def _traffic(workload, launch):
+    """Bytes per launch of the step's launch number `launch` (issue order within
+    a step, as `python -m fuseml_amd.profiling traffic --per-step N` numbers
+    them), or None."""
     path = TRAFFIC_SUMMARY.format(workload=workload)
-    if grid_threads is None or not os.path.exists(path):
+    if not os.path.exists(path):
         return None
     text = open(path).read()
     if "```json" not in text:
         return None
     data = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
     for k in data.get("kernels", []):
-        if k.get("grid") == grid_threads and k.get("fetch_bytes") is not None and k.get("write_bytes") is not None:
+        if (str(k.get("kernel", "")).startswith("gemm_epilogue_kernel") and k.get("launch") == launch
+                and k.get("fetch_bytes") is not None and k.get("write_bytes") is not None):
             return int(k["fetch_bytes"] + k["write_bytes"])
     return None
 
@@ -320,7 +307,7 @@ def main():
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": _traffic(name, _grid_of(stages[dom][1], Mg, Ng)),
+            "traffic": _traffic(name, dom),
         },
         "cpu_baseline": cpu,
     }

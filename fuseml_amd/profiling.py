@@ -1,12 +1,15 @@
 """Summaries of rocprofv3 output for the fused kernels.
 
-    python -m fuseml_amd.profiling trace <kernel_trace.csv>
+    python -m fuseml_amd.profiling trace <kernel_trace.csv> [--per-step N]
     python -m fuseml_amd.profiling traffic <fetch counter_collection.csv> <write counter_collection.csv> \
-        --copy-mib 512
+        --copy-mib 512 [--per-step N]
 
-``trace`` groups dispatches by (kernel, grid size) — the G1 and G2 GEMMs of
-one block are the same template at different grids — and prints call count
-and average / min / max duration.
+``trace`` groups dispatches by (kernel, grid size, launch) and prints call
+count and average / min / max duration.  The GEMMs of one step are often the
+same template at the same grid (the 256-wide variants launch one workgroup per
+CU whatever the tile count), so ``--per-step N`` (N launches of the kernel per
+step, as ``bench.py`` prints in ``config.gemms_MNK``) numbers a kernel's
+dispatches in issue order and groups dispatch i as launch i % N.
 
 ``traffic`` turns the per-dispatch ``FETCH_SIZE`` and ``WRITE_SIZE`` counters
 (KiB) into bytes per launch.  The counters are scaled by what they read for a
@@ -37,38 +40,50 @@ def _short(name: str) -> str:
     return name[:60]
 
 
-def trace_summary(path: str) -> List[Dict[str, object]]:
+def _launch_positions(rows: List[Dict[str, str]], per_step: int) -> List[int]:
+    """Position (dispatch index mod per_step) of each row among the fused
+    kernel's dispatches in issue order (Dispatch_Id); 0 for other kernels."""
+    order = sorted((int(r.get("Dispatch_Id") or 0), i) for i, r in enumerate(rows)
+                   if "gemm_epilogue_kernel" in r["Kernel_Name"])
+    pos = [0] * len(rows)
+    for n, (_, i) in enumerate(order):
+        pos[i] = n % max(per_step, 1)
+    return pos
+
+
+def trace_summary(path: str, per_step: int = 1) -> List[Dict[str, object]]:
     rows = list(csv.DictReader(open(path)))
-    groups: Dict[Tuple[str, int], List[float]] = defaultdict(list)
-    for r in rows:
+    pos = _launch_positions(rows, per_step)
+    groups: Dict[Tuple[str, int, int], List[float]] = defaultdict(list)
+    for r, p in zip(rows, pos):
         grid = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0)
         dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # us
-        groups[(r["Kernel_Name"], grid)].append(dur)
+        groups[(r["Kernel_Name"], grid, p)].append(dur)
     out = []
-    for (name, grid), durs in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        out.append({"kernel": _short(name), "grid": grid, "calls": len(durs),
+    for (name, grid, p), durs in sorted(groups.items(), key=lambda kv: (kv[0][0], kv[0][2], -sum(kv[1]))):
+        out.append({"kernel": _short(name), "grid": grid, "launch": p, "calls": len(durs),
                     "avg_us": round(statistics.mean(durs), 2), "min_us": round(min(durs), 2),
                     "max_us": round(max(durs), 2)})
     return out
 
 
-def counter_by_dispatch(path: str, counter: str) -> Dict[Tuple[str, int], List[float]]:
-    rows = list(csv.DictReader(open(path)))
-    acc: Dict[Tuple[str, int], List[float]] = defaultdict(list)
-    for r in rows:
-        if r["Counter_Name"] != counter:
-            continue
-        acc[(r["Kernel_Name"], int(r.get("Grid_Size") or r.get("Grid_Size_X") or 0))].append(float(r["Counter_Value"]))
+def counter_by_dispatch(path: str, counter: str, per_step: int = 1) -> Dict[Tuple[str, int, int], List[float]]:
+    rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+    pos = _launch_positions(rows, per_step)
+    acc: Dict[Tuple[str, int, int], List[float]] = defaultdict(list)
+    for r, p in zip(rows, pos):
+        acc[(r["Kernel_Name"], int(r.get("Grid_Size") or r.get("Grid_Size_X") or 0), p)].append(
+            float(r["Counter_Value"]))
     return acc
 
 
-def traffic_summary(fetch_csv: str, write_csv: str, copy_mib: float) -> Dict[str, object]:
-    fetch = counter_by_dispatch(fetch_csv, "FETCH_SIZE")
-    write = counter_by_dispatch(write_csv, "WRITE_SIZE")
+def traffic_summary(fetch_csv: str, write_csv: str, copy_mib: float, per_step: int = 1) -> Dict[str, object]:
+    fetch = counter_by_dispatch(fetch_csv, "FETCH_SIZE", per_step)
+    write = counter_by_dispatch(write_csv, "WRITE_SIZE", per_step)
     copy_bytes = copy_mib * 1024 * 1024
 
     def copy_factor(table):
-        vals = [v for (n, _), vs in table.items() if COPY_KERNEL_HINT in n for v in vs]
+        vals = [v for (n, _, _), vs in table.items() if COPY_KERNEL_HINT in n for v in vs]
         big = [v for v in vals if v * 1024 > 0.5 * copy_bytes]
         if not big:
             return None
@@ -77,13 +92,13 @@ def traffic_summary(fetch_csv: str, write_csv: str, copy_mib: float) -> Dict[str
     ff, wf = copy_factor(fetch), copy_factor(write)
     kernels = []
     for key in sorted(set(fetch) | set(write)):
-        name, grid = key
+        name, grid, p = key
         if COPY_KERNEL_HINT in name:
             continue
         f = statistics.mean(fetch.get(key, [0.0])) * 1024
         w = statistics.mean(write.get(key, [0.0])) * 1024
         kernels.append({
-            "kernel": _short(name), "grid": grid,
+            "kernel": _short(name), "grid": grid, "launch": p,
             "fetch_bytes_raw": f, "write_bytes_raw": w,
             "fetch_bytes": None if ff is None else f * ff,
             "write_bytes": None if wf is None else w * wf,
@@ -96,16 +111,18 @@ def main(argv=None) -> int:
     sub = ap.add_subparsers(dest="cmd", required=True)
     t = sub.add_parser("trace")
     t.add_argument("csv")
+    t.add_argument("--per-step", type=int, default=1)
     tr = sub.add_parser("traffic")
     tr.add_argument("fetch_csv")
     tr.add_argument("write_csv")
     tr.add_argument("--copy-mib", type=float, required=True)
+    tr.add_argument("--per-step", type=int, default=1)
     a = ap.parse_args(argv)
     if a.cmd == "trace":
-        for row in trace_summary(a.csv):
+        for row in trace_summary(a.csv, a.per_step):
             print(json.dumps(row))
     else:
-        print(json.dumps(traffic_summary(a.fetch_csv, a.write_csv, a.copy_mib), indent=1))
+        print(json.dumps(traffic_summary(a.fetch_csv, a.write_csv, a.copy_mib, a.per_step), indent=1))
     return 0
 
 

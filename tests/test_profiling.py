@@ -1,0 +1,65 @@
+"""The rocprofv3 summaries used for the committed profiles (CPU only)."""
+
+import csv
+
+from fuseml_amd.profiling import trace_summary, traffic_summary
+
+GEMM = "_ZN12_GLOBAL__N_120gemm_epilogue_kernelILi256ELi256ELi32ELi4ELi2ELi4ELi1EDF16bEEv16fuseml_gemm_desc"
+COPY = "__amd_rocclr_copyBuffer"
+
+
+def _write(path, fields, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        w.writerows(rows)
+
+
+def test_trace_launches_grouped_by_position(tmp_path):
+    # Three steps of two launches at the same grid (G1 100 us, G2 50 us), with
+    # another kernel in between; rows out of dispatch order.
+    rows = []
+    did = 0
+    for step in range(3):
+        for pos, dur in ((0, 100_000), (1, 50_000)):
+            did += 1
+            rows.append({"Dispatch_Id": did, "Kernel_Name": GEMM, "Grid_Size_X": 131072,
+                         "Start_Timestamp": 1000 * did, "End_Timestamp": 1000 * did + dur + step})
+            did += 1
+            rows.append({"Dispatch_Id": did, "Kernel_Name": "other", "Grid_Size_X": 64,
+                         "Start_Timestamp": 1000 * did, "End_Timestamp": 1000 * did + 7000})
+    rows.reverse()
+    p = tmp_path / "t_kernel_trace.csv"
+    _write(p, ["Dispatch_Id", "Kernel_Name", "Grid_Size_X", "Start_Timestamp", "End_Timestamp"], rows)
+
+    merged = [r for r in trace_summary(str(p)) if r["kernel"].startswith("gemm_epilogue_kernel")]
+    assert len(merged) == 1 and merged[0]["calls"] == 6
+
+    split = {r["launch"]: r for r in trace_summary(str(p), per_step=2)
+             if r["kernel"] == "gemm_epilogue_kernel<256,256,32,4,2,4,1,bf16>"}
+    assert sorted(split) == [0, 1]
+    assert split[0]["calls"] == 3 and split[0]["avg_us"] == 100.0 and split[0]["max_us"] == 100.0
+    assert split[1]["calls"] == 3 and split[1]["avg_us"] == 50.0 and split[1]["min_us"] == 50.0
+
+
+def test_traffic_scaled_by_copy_and_split_by_launch(tmp_path):
+    fields = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"]
+    # Copy of 512 MiB read as 409.6 MiB by the counter: factor 1.25.
+    copy_kib = 512 * 1024 / 1.25
+    fetch = [{"Dispatch_Id": 1, "Kernel_Name": COPY, "Grid_Size": 512, "Counter_Name": "FETCH_SIZE",
+              "Counter_Value": copy_kib}]
+    write = [{"Dispatch_Id": 1, "Kernel_Name": COPY, "Grid_Size": 512, "Counter_Name": "WRITE_SIZE",
+              "Counter_Value": copy_kib}]
+    for i, (f, w) in enumerate([(10.0, 1.0), (20.0, 2.0)] * 2):
+        fetch.append({"Dispatch_Id": 2 + i, "Kernel_Name": GEMM, "Grid_Size": 131072,
+                      "Counter_Name": "FETCH_SIZE", "Counter_Value": f})
+        write.append({"Dispatch_Id": 2 + i, "Kernel_Name": GEMM, "Grid_Size": 131072,
+                      "Counter_Name": "WRITE_SIZE", "Counter_Value": w})
+    pf, pw = tmp_path / "f.csv", tmp_path / "w.csv"
+    _write(pf, fields, fetch)
+    _write(pw, fields, write)
+    t = traffic_summary(str(pf), str(pw), 512, per_step=2)
+    assert abs(t["fetch_factor"] - 1.25) < 1e-12 and abs(t["write_factor"] - 1.25) < 1e-12
+    k = {r["launch"]: r for r in t["kernels"]}
+    assert abs(k[0]["fetch_bytes"] - 10.0 * 1024 * 1.25) < 1e-6 and abs(k[0]["write_bytes"] - 1.0 * 1024 * 1.25) < 1e-6
+    assert abs(k[1]["fetch_bytes"] - 20.0 * 1024 * 1.25) < 1e-6 and abs(k[1]["write_bytes"] - 2.0 * 1024 * 1.25) < 1e-6
