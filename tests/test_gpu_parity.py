@@ -297,6 +297,37 @@ def test_variant_fp16_chain(forced_variant, shape):
     assert np.allclose(got, ref_sat, rtol=RTOL, atol=ATOL * 3.0e4)
 
 
+@pytest.mark.parametrize("forced_variant", ["large", "deep"], indirect=True)
+@pytest.mark.parametrize("shape,axis", [((4392, 4360, 136), 1), ((3996, 5112, 72), 0)],
+                         ids=["324tiles-rows", "320tiles-cols"])
+def test_variant_persistent_rounds(forced_variant, shape, axis):
+    """More tiles than workgroups: the 256-wide variants launch one workgroup per
+    CU and loop over the tiles in rounds.  324 tiles leave a last round of 68
+    (not a multiple of the 8 XCDs: plain order), 320 tiles one of 64 (XCD
+    order); ragged M and N, a staged residual and reductions that accumulate
+    across the rounds."""
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=41)
+    bias = (torch.rand(N, generator=_gen(42)) - 0.5).to(dtype)
+    resid = torch.randn(M, N, generator=_gen(43)).to(dtype)
+    inputs = [bias, resid, a, w.t()]
+    steps = [("add", 0, 1.0), ("add", 1, 1.0), ("gelu_erf", -1, 1.0)]
+    spec = _spec(left=2, right=3, ops=steps, out_dtype=dtype, store_tile=True,
+                 reductions=("sum", "amax", "mean"), reduce_axis=axis,
+                 reduce_dtypes=(torch.float32,) * 3,
+                 outputs=(("tile",), ("red", "sum"), ("red", "amax"), ("red", "mean")))
+    print(f"case variant={forced_variant} persistent rounds shape={shape} axis={axis}", flush=True)
+    tile, s, mx, mean = _launcher(spec, len(inputs))(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], 2, 3, steps, ("sum", "amax", "mean"), axis)
+    v = ref["tile"]
+    _check_tile(tile, v, f"{forced_variant} tile")
+    _check_red(s, ref["sum"], np.abs(v).sum(axis=axis), "sum")
+    _check_red(mx, ref["amax"], np.abs(v).max(axis=axis), "amax")
+    _check_red(mean, ref["mean"], np.abs(v).mean(axis=axis), "mean")
+
+
 def test_escape_store_and_tile_with_reductions():
     """mm -> relu (escapes) -> row sum/amax/mean: the C4 group shape, small."""
     M, N, K = 320, 640, 256
