@@ -18,10 +18,13 @@
 //   * Stages are filled by the global -> LDS DMA (buffer_load_dwordx4 ... lds):
 //     no staging registers, and an out-of-range offset returns zeros, which masks
 //     the M/N/K edges with no branches.
-//   * Three K-loop schedules (template parameter SCHED), one per tile variant:
+//   * Four K-loop schedules (template parameter SCHED), one per tile variant:
 //     256x256 ping-pong (8 waves, two groups alternating memory and compute
 //     phases, BK=32, 4 stages), 256x256 one wave per SIMD (4 waves, 128x128
-//     accumulators in AGPRs, BK=64, 2 stages), and 128x128 lock-step.
+//     accumulators in AGPRs, BK=64, 2 stages) in two forms (one k-step of
+//     fragments read ahead, or a whole stage of fragments read during its
+//     first k-step so that the next stage's DMA spreads over the other three),
+//     and 128x128 lock-step.
 //   * MFMA roles are swapped (MFMA "A" = rows of W, MFMA "B" = rows of x) so that
 //     each lane's accumulator holds one output row m and runs of 4 consecutive
 //     columns n; a row reduction needs a single cross-half-wave exchange.
@@ -406,9 +409,10 @@ __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, 
 // SCHED selects the K-loop schedule: 0 lock-step waves, 1 ping-pong (8 waves,
 // two per SIMD), 3 one wave per SIMD (4 waves, 128x128 wave tiles, accumulators
 // in AGPRs) with two deep stages (BK=64), the barrier before each stage's last
-// k-step and each stage's DMA split over two k-steps.
+// k-step and each stage's DMA split over two k-steps, 6 the same tile with a
+// whole stage of fragments in registers (described at its loop).
 template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T>
-__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED == 3 ? 1 : 2)))
+__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED >= 3 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   using G = StageGeom<BK>;
   constexpr int NW = WM * WN;  // waves per workgroup
@@ -547,13 +551,15 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     uint32_t op_bytes = a_bytes;
     uint32_t op_o[kOpDma ? LPS : 1];  // chunk c's byte offset in its slot (kOOB: column past N)
     uint64_t op_row_bytes = 0;        // operand row pitch in bytes
+    uint32_t op_osm = 0;
     if constexpr (kOpDma) {
       const int si = staged >= 0 ? staged : 0;
       op_ptr = d.operands[si].ptr;
       op_bytes = (uint32_t)(d.operands[si].extent * 2);
       const uint32_t osm = (uint32_t)d.operands[si].stride_m;
+      op_osm = osm;
       op_row_bytes = (uint64_t)osm * 2u;
-      static_for<0, LPS>([&](auto c) {
+      if constexpr (SCHED != 6) static_for<0, LPS>([&](auto c) {
         const int r = (wave + NW * c) * RPD + lane / CPR;
         const int n = n0 + 8 * ((lane % CPR) ^ (r & 31));
         op_o[c] = n < N ? ((uint32_t)(m0 + r) * osm + (uint32_t)n) * 2u : kOOB;
@@ -572,8 +578,16 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       const __amdgpu_buffer_rsrc_t rop = make_rsrc(op_slot_ptr(slot), op_slot_bytes(slot));
       char* st = smem + slot * STAGE;
       static_for<decltype(c0)::value, decltype(c1)::value>([&](auto c) {
+        uint32_t oo;
+        if constexpr (SCHED == 6) {  // computed here: 16 fewer registers held across the K loop
+          const int r = (wave + NW * c) * RPD + lane / CPR;
+          const int n = n0 + 8 * ((lane % CPR) ^ (r & 31));
+          oo = n < N ? ((uint32_t)(m0 + r) * op_osm + (uint32_t)n) * 2u : kOOB;
+        } else {
+          oo = op_o[c];
+        }
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rop, (__attribute__((address_space(3))) void*)(st + (wave + NW * c) * 1024), 16, op_o[c], 0, 0, 0);
+            rop, (__attribute__((address_space(3))) void*)(st + (wave + NW * c) * 1024), 16, oo, 0, 0, 0);
       });
     };
 
@@ -615,11 +629,16 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         uint32_t off;
         __amdgpu_buffer_rsrc_t r;
         if constexpr (c < A_DMA) {
-          off = (k0 + a_k[c] < K) ? a_off[c] + kb : kOOB;
+          // The whole-stage schedule runs only for K % 64 == 0 (choose_config):
+          // a stage is wholly inside or outside [0, K), and the per-chunk k
+          // offsets need no registers across its K loop.
+          if constexpr (SCHED == 6) off = kt < nk ? a_off[c] + kb : kOOB;
+          else off = (k0 + a_k[c] < K) ? a_off[c] + kb : kOOB;
           r = ra;
         } else {
           constexpr int i = c - A_DMA;
-          off = (k0 + b_k[i] < K) ? b_off[i] + kb : kOOB;
+          if constexpr (SCHED == 6) off = kt < nk ? b_off[i] + kb : kOOB;
+          else off = (k0 + b_k[i] < K) ? b_off[i] + kb : kOOB;
           r = rb;
         }
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -692,7 +711,91 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
     };
-    if constexpr (SCHED == 3) {
+    if constexpr (SCHED == 6) {
+      // One wave per SIMD, two stages of BK=64, a whole stage's fragments in
+      // registers.  Stage k (slot k % 2):
+      //   k-step 0: MFMAs while the fragments of k-steps 1-3 are read;
+      //   barrier 1 (after this wave's reads): no wave reads slot k % 2 any more;
+      //   k-steps 1-3: MFMAs while stage k+2's DMA goes into slot k % 2, spread
+      //   over the three k-steps (barrier 2 before k-step 3: stage k+1 landed
+      //   and visible); k-step 3 also reads stage k+1's k-step 0 fragments.
+      // Each k-step then carries at most ~21 KB of DMA writes or 24 KB of reads
+      // per wave-quad, instead of two k-steps carrying both.
+      static_assert(S == 2 && KS == 4 && NI == 4 && NJ == 4 && LPS == 16, "one-wave whole-stage geometry");
+      i32x4_t fr[KS][NI + NJ];
+      auto rd = [&](const char* st, auto ks, auto f) {
+        const int chunk = ((2 * ks + khalf) ^ swz) << 4;
+        if constexpr (f < NI)
+          fr[ks][f] = *reinterpret_cast<const i32x4_t*>(st + fa_row + 32 * f * RB + chunk);
+        else
+          fr[ks][f] = *reinterpret_cast<const i32x4_t*>(st + fb_row + 32 * (f - NI) * RB + chunk);
+      };
+      auto issue = [&](int kt, int slot, auto c0, auto c1, auto tail) {
+        if constexpr (decltype(tail)::value) {
+          if (op_dma && kt >= nk) {
+            load_op_chunks(slot, c0, c1);
+            return;
+          }
+        }
+        load_chunks(kt, slot, c0, c1);
+      };
+      // k-step ks: MFMAs from fr[ks]; fragment reads [r0, r1) of stage `rst`
+      // (read r: k-step r / 8, fragment r % 8) and DMA chunks [c0, c1) of stage
+      // kt, each spread evenly over the 16 MFMAs.
+      auto kstep = [&](auto ks, const char* rst, auto r0, auto r1, int kt, int slot, auto c0, auto c1, auto tail) {
+        constexpr int n_rd = decltype(r1)::value - decltype(r0)::value;
+        constexpr int n_dma = decltype(c1)::value - decltype(c0)::value;
+        static_for<0, NI * NJ>([&](auto q) {
+          constexpr int i = q / NJ, j = q % NJ;
+          acc[i][j] = mfma32<T>(fr[ks][i], fr[ks][NI + j], acc[i][j]);
+          static_for<0, n_rd>([&](auto m) {
+            if constexpr ((m * (NI * NJ)) / n_rd == q) {
+              constexpr int r = decltype(r0)::value + m;
+              rd(rst, std::integral_constant<int, r / 8>{}, std::integral_constant<int, r % 8>{});
+            }
+          });
+          static_for<0, n_dma>([&](auto m) {
+            if constexpr ((m * (NI * NJ)) / n_dma == q) {
+              constexpr int c = decltype(c0)::value + m;
+              issue(kt, slot, std::integral_constant<int, c>{}, std::integral_constant<int, c + 1>{}, tail);
+            }
+          });
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      using R0 = std::integral_constant<int, 0>;
+      using R8 = std::integral_constant<int, 8>;
+      using R32 = std::integral_constant<int, 32>;
+      using D6 = std::integral_constant<int, 6>;
+      using D11 = std::integral_constant<int, 11>;
+      using D16 = std::integral_constant<int, 16>;
+      auto body = [&](int k, auto tail) {
+        const char* st = smem + (k & 1) * STAGE;
+        const char* nst = smem + ((k + 1) & 1) * STAGE;
+        kstep(I0{}, st, R8{}, R32{}, k + 2, k & 1, R0{}, R0{}, tail);
+        wait_lgkmcnt0();
+        barrier();  // slot k % 2 retired
+        kstep(I1{}, st, R0{}, R0{}, k + 2, k & 1, R0{}, D6{}, tail);
+        kstep(I2{}, st, R0{}, R0{}, k + 2, k & 1, D6{}, D11{}, tail);
+        wait_vmcnt<11>();  // stage k+1 (only stage k+2's first 11 chunks are younger)
+        barrier();
+        kstep(I3{}, nst, R0{}, R8{}, k + 2, k & 1, D11{}, D16{}, tail);
+      };
+      using Tail = std::true_type;
+      issue(0, 0, R0{}, D16{}, Tail{});
+      issue(1, 1, R0{}, D16{}, Tail{});
+      wait_vmcnt<16>();  // stage 0
+      barrier();
+      static_for<0, NI + NJ>([&](auto f) { rd(smem, I0{}, f); });
+      const int steady = op_dma ? nk - 2 : nk;
+      int k = 0;
+      for (; k < steady; ++k) body(k, std::false_type{});
+      for (; k < nk; ++k) body(k, Tail{});
+    } else if constexpr (SCHED == 3) {
       // One wave per SIMD, two stages of BK=64 (four MFMA k-steps each).  Stage k:
       //   k-steps 0..2: MFMAs of k-step s while k-step s+1's fragments are read;
       //   under k-step 0 the second half of stage k+1's DMA is issued (into
@@ -1243,7 +1346,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         });
       }
     };
-    if constexpr (SCHED == 3) {
+    if constexpr (SCHED >= 3) {
       // A runtime loop over the column blocks, so that the op code exists once
       // (not NI times: at NI = 4 the copies cost instruction-cache misses on
       // every tile).  Each block is copied out of the AGPRs by a uniform branch
@@ -1364,26 +1467,34 @@ struct TileConfig {
 constexpr TileConfig kLarge = {256, 256, 32, 4, 2, 4, 1};  // 8 waves ping-pong, 132 KB LDS, 1 WG/CU
 constexpr TileConfig kDeep = {256, 256, 64, 2, 2, 2, 3};   // 4 waves (1/SIMD), BK=64 x 2 stages, 132 KB LDS
 constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2, 0};  // 4 waves lock-step, 66 KB LDS, 2 WG/CU
+constexpr TileConfig kDeep3 = {256, 256, 64, 2, 2, 2, 6};  // as kDeep, whole-stage fragments; K % 64 == 0
 
 constexpr int64_t kMaxBytes = (int64_t)1 << 31;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-TileConfig choose_config(const fuseml_gemm_desc& d) {
-  // FUSEML_HIP_TILE=large|deep|small pins a variant (tuning sweeps).
+// `cus`: the device's CU count (the 256-wide variants run one workgroup per CU).
+TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
+  // FUSEML_HIP_TILE=large|deep|deep3|small pins a variant (tuning sweeps;
+  // deep3 falls back to deep when K % 64 != 0).
   if (const char* force = getenv("FUSEML_HIP_TILE")) {
     if (!strcmp(force, "large")) return kLarge;
     if (!strcmp(force, "deep")) return kDeep;
     if (!strcmp(force, "small")) return kSmall;
+    if (!strcmp(force, "deep3")) return d.K % 64 == 0 ? kDeep3 : kDeep;
   }
   // A 256x256 tile keeps the LDS traffic per MFMA low enough for the MFMA pipe
   // to stay busy; below one full wave of 256-tile work the 128x128 variant
-  // fills more CUs.  Of the two 256x256 schedules, the one-wave-per-SIMD one
-  // has the faster K loop but the slower epilogue (no second wave on a SIMD to
-  // overlap its latencies): it wins once K is long enough to amortize that,
-  // about K >= 8192 on the measured shapes.
+  // fills more CUs.  Of the 256x256 schedules, the one-wave-per-SIMD ones have
+  // the faster K loop but the slower epilogue (no second wave on a SIMD to
+  // overlap its latencies).  The whole-stage one wins from K = 2048 when each
+  // CU runs several tiles (C4 2%, C5 4-10%) or from K = 8192; with a single
+  // round of tiles at K = 4096 (C2's second GEMM: 256 tiles, a residual) its
+  // exposed epilogue loses 0-5%, and at K = 1024 it loses 7-19%.  With
+  // K % 64 != 0 the two-stage one takes over from K = 8192.
   const int64_t large_tiles = cdiv(d.M, 256) * cdiv(d.N, 256);
   if (large_tiles < 128) return kSmall;
+  if (d.K % 64 == 0 && (d.K >= 8192 || (d.K >= 2048 && large_tiles > cus))) return kDeep3;
   return d.K >= 8192 ? kDeep : kLarge;
 }
 
@@ -1567,51 +1678,6 @@ hipError_t launch_variant(const fuseml_gemm_desc& d, hipStream_t stream, int max
   return hipGetLastError();
 }
 
-}  // namespace
-
-extern "C" {
-
-const char* fuseml_last_error(void) { return g_last_error; }
-
-int fuseml_abi_version(void) { return FUSEML_ABI_VERSION; }
-
-size_t fuseml_desc_size(void) { return sizeof(fuseml_gemm_desc); }
-
-int fuseml_gemm_epilogue_supported(const fuseml_gemm_desc* desc) {
-  g_last_error[0] = '\0';
-  return validate(desc) == FUSEML_OK ? 1 : 0;
-}
-
-int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]) {
-  g_last_error[0] = '\0';
-  const int rc = validate(desc);
-  if (rc != FUSEML_OK) return rc;
-  const TileConfig c = choose_config(*desc);
-  cfg[0] = c.bm;
-  cfg[1] = c.bn;
-  cfg[2] = c.wm * c.wn;
-  cfg[3] = c.lds_bytes();
-  return FUSEML_OK;
-}
-
-int fuseml_device_arch(int device, char* buf, int buflen) {
-  hipDeviceProp_t prop;
-  const hipError_t e = hipGetDeviceProperties(&prop, device);
-  if (e != hipSuccess) {
-    set_error("hipGetDeviceProperties: %s", hipGetErrorString(e));
-    return FUSEML_EHIP;
-  }
-  if (buf != nullptr && buflen > 0) {
-    strncpy(buf, prop.gcnArchName, (size_t)buflen - 1);
-    buf[buflen - 1] = '\0';
-  }
-  return FUSEML_OK;
-}
-
-}  // extern "C"
-
-namespace {
-
 // Per-device check and CU count, queried once per device: the CU count for a
 // gfx950 device, else FUSEML_EDEVICE or FUSEML_EHIP (negative; the error is set).
 constexpr int kMaxDevices = 64;
@@ -1641,6 +1707,49 @@ int device_cus(int dev) {
 }  // namespace
 
 extern "C" {
+
+const char* fuseml_last_error(void) { return g_last_error; }
+
+int fuseml_abi_version(void) { return FUSEML_ABI_VERSION; }
+
+size_t fuseml_desc_size(void) { return sizeof(fuseml_gemm_desc); }
+
+int fuseml_gemm_epilogue_supported(const fuseml_gemm_desc* desc) {
+  g_last_error[0] = '\0';
+  return validate(desc) == FUSEML_OK ? 1 : 0;
+}
+
+int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]) {
+  g_last_error[0] = '\0';
+  const int rc = validate(desc);
+  if (rc != FUSEML_OK) return rc;
+  // The CU count of the current device if it is known, else MI355X's.
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) {
+    const int known = g_device_cus[dev].load(std::memory_order_relaxed);
+    if (known > 0) cus = known;
+  }
+  const TileConfig c = choose_config(*desc, cus);
+  cfg[0] = c.bm;
+  cfg[1] = c.bn;
+  cfg[2] = c.wm * c.wn;
+  cfg[3] = c.lds_bytes();
+  return FUSEML_OK;
+}
+
+int fuseml_device_arch(int device, char* buf, int buflen) {
+  hipDeviceProp_t prop;
+  const hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) {
+    set_error("hipGetDeviceProperties: %s", hipGetErrorString(e));
+    return FUSEML_EHIP;
+  }
+  if (buf != nullptr && buflen > 0) {
+    strncpy(buf, prop.gcnArchName, (size_t)buflen - 1);
+    buf[buflen - 1] = '\0';
+  }
+  return FUSEML_OK;
+}
 
 int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
   g_last_error[0] = '\0';
@@ -1675,11 +1784,13 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
     }
   }
 
-  const TileConfig c = choose_config(d);
+  const TileConfig c = choose_config(d, cus);
   if (c.sched == kDeep.sched)
     e = launch_variant<kDeep>(d, stream, cus);
   else if (c.sched == kLarge.sched)
     e = launch_variant<kLarge>(d, stream, cus);
+  else if (c.sched == kDeep3.sched)
+    e = launch_variant<kDeep3>(d, stream, cus);
   else
     e = launch_variant<kSmall>(d, stream, 0);
   if (e != hipSuccess) {

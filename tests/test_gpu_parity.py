@@ -159,11 +159,20 @@ def test_reductions_parity(axis, shape):
 # Every kernel variant (tile size and K-loop schedule), forced through
 # FUSEML_HIP_TILE, which the library reads at each launch.  The automatic choice
 # picks the 256x256 variants only at large sizes, so these cases are what pins
-# the ping-pong ("large") and one-wave-per-SIMD ("deep", BK=64) schedules on
-# every chain, on ragged edges and on K that ends mid-stage.
+# the ping-pong ("large") and one-wave-per-SIMD ("deep", "deep3"; BK=64)
+# schedules on every chain, on ragged edges and on K that ends mid-stage.
 # ---------------------------------------------------------------------------
 
-VARIANTS = ["large", "deep", "small"]
+VARIANTS = ["large", "deep", "deep3", "small"]
+
+
+def _k_for(variant, K):
+    """deep3 (the one-wave schedule with whole-stage fragments) runs only for
+    K % 64 == 0 (the library falls back to deep otherwise), so its cases keep
+    the ragged M and N and round K up to a multiple of 64."""
+    return -(-K // 64) * 64 if variant == "deep3" else K
+
+
 VARIANT_SHAPES = [
     (600, 1030, 200),   # ragged M and N, K ends mid-stage (BK=32 and BK=64)
     (257, 512, 72),     # one row past a 256 tile, K = one BK=64 stage + 8
@@ -183,6 +192,7 @@ def forced_variant(request, monkeypatch):
 @pytest.mark.parametrize("shape", VARIANT_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_variant_chain_parity(forced_variant, chain, shape):
     M, N, K = shape
+    K = _k_for(forced_variant, K)
     dtype = torch.bfloat16
     a, w = _gemm_inputs(M, N, K, dtype, seed=21)
     ops = _operands(M, N, dtype, seed=22)
@@ -200,7 +210,7 @@ def test_variant_chain_parity(forced_variant, chain, shape):
 @pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
 @pytest.mark.parametrize("axis", [1, 0])
 def test_variant_reductions_parity(forced_variant, axis):
-    M, N, K = 600, 1030, 200
+    M, N, K = 600, 1030, _k_for(forced_variant, 200)
     dtype = torch.bfloat16
     a, w = _gemm_inputs(M, N, K, dtype, seed=23)
     bias = (torch.rand(N, generator=_gen(24)) - 0.5).to(dtype)
@@ -229,6 +239,7 @@ def test_variant_reductions_with_tile_operand(forced_variant, axis, store_tile, 
     """Reductions after a 2-D (LDS-staged) residual: the reduction partials reuse
     the staging tile's LDS, with and without a staged output."""
     M, N, K = shape
+    K = _k_for(forced_variant, K)
     dtype = torch.bfloat16
     a, w = _gemm_inputs(M, N, K, dtype, seed=25)
     bias = (torch.rand(N, generator=_gen(26)) - 0.5).to(dtype)
@@ -260,6 +271,7 @@ def test_variant_tile_operand_short_k(forced_variant, K):
     """A 2-D operand with K of zero to a few stages: every way the staged
     operand's LDS slots can be left free by a short K loop."""
     M, N = 520, 776
+    K = _k_for(forced_variant, K)
     dtype = torch.bfloat16
     a, w = _gemm_inputs(M, N, K, dtype, seed=28)
     ops = _operands(M, N, dtype, seed=29)
@@ -280,6 +292,7 @@ def test_variant_fp16_chain(forced_variant, shape):
     """fp16 GEMM operands (f16 MFMA), an fp16 residual through the staging tile
     and an fp16 staged output, saturated at +-65504, on every variant."""
     M, N, K = shape
+    K = _k_for(forced_variant, K)
     dtype = torch.float16
     a, w = _gemm_inputs(M, N, K, dtype, seed=31)
     bias = (torch.rand(N, generator=_gen(32)) - 0.5).to(dtype)
@@ -297,7 +310,7 @@ def test_variant_fp16_chain(forced_variant, shape):
     assert np.allclose(got, ref_sat, rtol=RTOL, atol=ATOL * 3.0e4)
 
 
-@pytest.mark.parametrize("forced_variant", ["large", "deep"], indirect=True)
+@pytest.mark.parametrize("forced_variant", ["large", "deep", "deep3"], indirect=True)
 @pytest.mark.parametrize("shape,axis", [((4392, 4360, 136), 1), ((3996, 5112, 72), 0)],
                          ids=["324tiles-rows", "320tiles-cols"])
 def test_variant_persistent_rounds(forced_variant, shape, axis):
@@ -307,6 +320,7 @@ def test_variant_persistent_rounds(forced_variant, shape, axis):
     order); ragged M and N, a staged residual and reductions that accumulate
     across the rounds."""
     M, N, K = shape
+    K = _k_for(forced_variant, K)
     dtype = torch.bfloat16
     a, w = _gemm_inputs(M, N, K, dtype, seed=41)
     bias = (torch.rand(N, generator=_gen(42)) - 0.5).to(dtype)
