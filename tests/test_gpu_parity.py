@@ -433,3 +433,27 @@ def test_c2_full_size_sampled_rows():
     # h is an exact bf16 round of G1; check it too
     ref_h = ora.gelu_erf(ora_w.linear(_np(x)[rows], _np(W1), _np(b1)))
     _check_tile(h[torch.as_tensor(rows).cuda()], ref_h, "C2 G1")
+
+
+def test_c5_block_full_size_sampled_rows():
+    """One C5 block at full size: G1 (K=4096, 2048 tiles) and G2 (K=16384, 512
+    tiles, residual) both on the one-wave whole-stage schedule, several tiles
+    per workgroup."""
+    from fuseml_amd.workloads import c5_stacked_mlp
+
+    wl = c5_stacked_mlp(num_blocks=1)
+    blk = wl.model.blocks[0]
+    x = wl.inputs[0]
+    W1, b1, W2, b2 = blk.linear1.weight, blk.linear1.bias, blk.linear2.weight, blk.linear2.bias
+    g1 = _launcher(_spec(left=1, right=2, ops=[("add", 0, 1.0), ("gelu_erf",)], out_dtype=x.dtype), 3)
+    g2 = _launcher(_spec(left=1, right=2, ops=[("add", 0, 1.0), ("add", 3, 1.0)], out_dtype=x.dtype), 4)
+    print("case C5 block full size", flush=True)
+    xd = x.cuda()
+    h = g1(b1.cuda(), xd, W1.t().cuda())
+    y = g2(b2.cuda(), h, W2.t().cuda(), xd)
+    torch.cuda.synchronize()
+    rows = _sample_rows(x.shape[0], n=24, seed=5)
+    ref = ora_w.transformer_mlp(_np(x), _np(W1), _np(b1), _np(W2), _np(b2), rows=rows)
+    _check_tile(y[torch.as_tensor(rows).cuda()], ref, "C5 block")
+    ref_h = ora.gelu_erf(ora_w.linear(_np(x)[rows], _np(W1), _np(b1)))
+    _check_tile(h[torch.as_tensor(rows).cuda()], ref_h, "C5 G1")
