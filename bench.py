@@ -56,6 +56,8 @@ def _parse():
     p.add_argument("--workload", default="C2", choices=sorted(WORKLOAD_DESC))
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--no-eager", action="store_true", help="skip the eager GPU comparison")
+    p.add_argument("--eager-only", action="store_true",
+                   help="run only the eager leg and print its call count (rocprof counter runs of the eager module)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--calib-copy-mb", type=int, default=0,
                    help="after timing, run device copies of this size (rocprof counter calibration)")
@@ -135,18 +137,65 @@ def _traffic(workload, launch):
     """Bytes per launch of the step's launch number `launch` (issue order within
     a step, as `python -m fuseml_amd.profiling traffic --per-step N` numbers
     them), or None."""
-    path = TRAFFIC_SUMMARY.format(workload=workload)
-    if not os.path.exists(path):
+    data = _json_block(TRAFFIC_SUMMARY.format(workload=workload))
+    if data is None:
         return None
-    text = open(path).read()
-    if "```json" not in text:
-        return None
-    data = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
     for k in data.get("kernels", []):
         if (str(k.get("kernel", "")).startswith("gemm_epilogue_kernel") and k.get("launch") == launch
                 and k.get("fetch_bytes") is not None and k.get("write_bytes") is not None):
             return int(k["fetch_bytes"] + k["write_bytes"])
     return None
+
+
+EAGER_TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "traffic_eager_{workload}.md")
+
+
+def _json_block(path):
+    if not os.path.exists(path):
+        return None
+    text = open(path).read()
+    if "```json" not in text:
+        return None
+    return json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+
+
+def _hbm_traffic(workload, gemms):
+    """Fused step against the eager module, both from committed counter summaries.
+
+    Final-output bytes are what any implementation must write (the last GEMM's
+    bf16 tile, plus C4's three fp32 reduction vectors); written bytes beyond
+    them are intermediates.  Each intermediate is written once and read back at
+    least once, so the share of intermediate writes removed is the share of
+    intermediate traffic removed."""
+    fused, eager = _json_block(TRAFFIC_SUMMARY.format(workload=workload)), _json_block(
+        EAGER_TRAFFIC_SUMMARY.format(workload=workload))
+    if fused is None or eager is None:
+        return None
+    gemm_entries = [k for k in fused["kernels"] if str(k["kernel"]).startswith("gemm_epilogue_kernel")]
+    if not gemm_entries or any(k.get("fetch_bytes") is None or k.get("write_bytes") is None
+                               for k in fused["kernels"]):
+        return None
+    # the summaries number a step's launches modulo their count of distinct shapes
+    reps = len(gemms) / len(gemm_entries)
+    f_fetch = f_write = 0.0
+    for k in fused["kernels"]:
+        r = reps if k in gemm_entries else 1.0
+        f_fetch += k["fetch_bytes"] * r
+        f_write += k["write_bytes"] * r
+    M, N, _ = gemms[-1]
+    out_bytes = M * N * 2 + (3 * M * 4 if workload == "C4" else 0)
+    e_fetch, e_write = eager["fetch_bytes_per_call"], eager["write_bytes_per_call"]
+    e_int, f_int = e_write - out_bytes, max(f_write - out_bytes, 0.0)
+    return {
+        "eager_bytes": int(e_fetch + e_write),
+        "fused_bytes": int(f_fetch + f_write),
+        "saved_frac": round(1.0 - (f_fetch + f_write) / (e_fetch + e_write), 4),
+        "eager_write_bytes": int(e_write),
+        "fused_write_bytes": int(f_write),
+        "final_output_bytes": int(out_bytes),
+        "intermediate_eliminated_frac": round(1.0 - f_int / e_int, 4) if e_int > 0 else None,
+        "source": f"profiles/traffic_{workload}.md, profiles/traffic_eager_{workload}.md",
+    }
 
 
 # ---------------------------------------------------------------------------
@@ -206,6 +255,33 @@ def _cpu_baseline(name, wl, seconds):
 # ---------------------------------------------------------------------------
 
 
+def _calib_copy(mb, dev):
+    """Device copies of `mb` MiB, the known-size reference for the rocprof
+    FETCH_SIZE / WRITE_SIZE scale factors."""
+    if mb <= 0:
+        return
+    src = torch.empty(mb * 1024 * 1024, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def _run_eager(wl, warmup, steps):
+    """The workload's module under PyTorch eager: (forward calls made, ms per timed call)."""
+    with torch.no_grad():
+        n_warm = max(3, warmup)
+        for _ in range(n_warm):
+            wl.model(*wl.inputs)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            wl.model(*wl.inputs)
+        torch.cuda.synchronize()
+    return n_warm + steps, (time.perf_counter() - t0) * 1e3 / steps
+
+
 def main():
     args = _parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -224,6 +300,12 @@ def main():
     wl = WORKLOADS[name]()
     wl.to(dev)
     torch.backends.cuda.matmul.allow_tf32 = False
+
+    if args.eager_only:
+        _calib_copy(args.calib_copy_mb, dev)
+        calls, eager_ms = _run_eager(wl, args.warmup, args.steps)
+        print(json.dumps({"workload": name, "eager_ms": round(eager_ms, 4), "eager_calls": calls}), flush=True)
+        return
 
     stages = _build_pipeline(name, wl, dev)
     with torch.no_grad():
@@ -256,26 +338,11 @@ def main():
     Mg, Ng, Kg = dk["gemm_MNK"]
     achieved = 2.0 * Mg * Ng * Kg / (dk["avg_ms"] * 1e-3) / 1e12
 
-    if args.calib_copy_mb > 0:
-        nbytes = args.calib_copy_mb * 1024 * 1024
-        src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    _calib_copy(args.calib_copy_mb, dev)
 
     eager_ms = None
     if not args.no_eager:
-        with torch.no_grad():
-            for _ in range(max(3, args.warmup)):
-                wl.model(*wl.inputs)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(args.steps):
-                wl.model(*wl.inputs)
-            torch.cuda.synchronize()
-            eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        _, eager_ms = _run_eager(wl, args.warmup, args.steps)
 
     cpu = None
     if not args.no_cpu:
@@ -309,6 +376,7 @@ def main():
             "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": _traffic(name, dom),
         },
+        "hbm_traffic": _hbm_traffic(name, wl.gemms),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -15,6 +15,11 @@ dispatches in issue order and groups dispatch i as launch i % N.
 (KiB) into bytes per launch.  The counters are scaled by what they read for a
 device-to-device copy of known size run in the same process
 (``bench.py --calib-copy-mb``): factor = copy bytes / counter bytes.
+
+``step-traffic`` sums the same counters over every dispatch of a run (the
+calibration copy aside) and divides by ``--calls``, the number of times the
+run called the module (``bench.py --eager-only`` prints it): HBM bytes per
+call of the eager module, whatever kernels the library picks.
 """
 
 from __future__ import annotations
@@ -77,19 +82,22 @@ def counter_by_dispatch(path: str, counter: str, per_step: int = 1) -> Dict[Tupl
     return acc
 
 
+def _copy_factor(table: Dict[Tuple[str, int, int], List[float]], copy_bytes: float):
+    """copy bytes / counter bytes read for the calibration copy, or None."""
+    vals = [v for (n, _, _), vs in table.items() if COPY_KERNEL_HINT in n for v in vs]
+    # FETCH_SIZE reads a device copy at about half its bytes: keep every dispatch
+    # of at least a quarter of the copy size.
+    big = [v for v in vals if v * 1024 >= 0.25 * copy_bytes]
+    if not big:
+        return None
+    return copy_bytes / (statistics.median(big) * 1024)
+
+
 def traffic_summary(fetch_csv: str, write_csv: str, copy_mib: float, per_step: int = 1) -> Dict[str, object]:
     fetch = counter_by_dispatch(fetch_csv, "FETCH_SIZE", per_step)
     write = counter_by_dispatch(write_csv, "WRITE_SIZE", per_step)
     copy_bytes = copy_mib * 1024 * 1024
-
-    def copy_factor(table):
-        vals = [v for (n, _, _), vs in table.items() if COPY_KERNEL_HINT in n for v in vs]
-        big = [v for v in vals if v * 1024 > 0.5 * copy_bytes]
-        if not big:
-            return None
-        return copy_bytes / (statistics.median(big) * 1024)
-
-    ff, wf = copy_factor(fetch), copy_factor(write)
+    ff, wf = _copy_factor(fetch, copy_bytes), _copy_factor(write, copy_bytes)
     kernels = []
     for key in sorted(set(fetch) | set(write)):
         name, grid, p = key
@@ -106,6 +114,39 @@ def traffic_summary(fetch_csv: str, write_csv: str, copy_mib: float, per_step: i
     return {"copy_mib": copy_mib, "fetch_factor": ff, "write_factor": wf, "kernels": kernels}
 
 
+def step_traffic(fetch_csv: str, write_csv: str, copy_mib: float, calls: int) -> Dict[str, object]:
+    """HBM bytes per call of a whole module (every dispatch but the calibration
+    copy), for a run that called the module ``calls`` times: totals over the
+    kernels dispatched at least once per call, scaled by the copy factors,
+    divided by ``calls``.  Used for the
+    eager leg, whose kernels (library GEMMs, elementwise ops) vary in name and
+    count from one torch build to the next."""
+    fetch = counter_by_dispatch(fetch_csv, "FETCH_SIZE")
+    write = counter_by_dispatch(write_csv, "WRITE_SIZE")
+    copy_bytes = copy_mib * 1024 * 1024
+    ff, wf = _copy_factor(fetch, copy_bytes), _copy_factor(write, copy_bytes)
+    kernels = []
+    for key in sorted(set(fetch) | set(write)):
+        name, grid, _ = key
+        if COPY_KERNEL_HINT in name:
+            continue
+        f, w = fetch.get(key, []), write.get(key, [])
+        kernels.append({
+            "kernel": _short(name), "grid": grid, "dispatches": max(len(f), len(w)),
+            "fetch_bytes_per_call": None if ff is None else sum(f) * 1024 * ff / calls,
+            "write_bytes_per_call": None if wf is None else sum(w) * 1024 * wf / calls,
+        })
+    # A kernel dispatched fewer times than the module was called is one-off work
+    # (library workspace fills, first-call set-up), not part of a call.
+    per_call = [x for x in kernels if x["dispatches"] >= calls]
+    tot = lambda k: None if any(x[k] is None for x in per_call) else sum(x[k] for x in per_call)  # noqa: E731
+    for x in kernels:
+        x["per_call"] = x["dispatches"] >= calls
+    return {"copy_mib": copy_mib, "fetch_factor": ff, "write_factor": wf, "calls": calls,
+            "fetch_bytes_per_call": tot("fetch_bytes_per_call"),
+            "write_bytes_per_call": tot("write_bytes_per_call"), "kernels": kernels}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -117,12 +158,19 @@ def main(argv=None) -> int:
     tr.add_argument("write_csv")
     tr.add_argument("--copy-mib", type=float, required=True)
     tr.add_argument("--per-step", type=int, default=1)
+    st = sub.add_parser("step-traffic")
+    st.add_argument("fetch_csv")
+    st.add_argument("write_csv")
+    st.add_argument("--copy-mib", type=float, required=True)
+    st.add_argument("--calls", type=int, required=True)
     a = ap.parse_args(argv)
     if a.cmd == "trace":
         for row in trace_summary(a.csv, a.per_step):
             print(json.dumps(row))
-    else:
+    elif a.cmd == "traffic":
         print(json.dumps(traffic_summary(a.fetch_csv, a.write_csv, a.copy_mib, a.per_step), indent=1))
+    else:
+        print(json.dumps(step_traffic(a.fetch_csv, a.write_csv, a.copy_mib, a.calls), indent=1))
     return 0
 
 

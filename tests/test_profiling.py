@@ -2,7 +2,7 @@
 
 import csv
 
-from fuseml_amd.profiling import trace_summary, traffic_summary
+from fuseml_amd.profiling import step_traffic, trace_summary, traffic_summary
 
 GEMM = "_ZN12_GLOBAL__N_120gemm_epilogue_kernelILi256ELi256ELi32ELi4ELi2ELi4ELi1EDF16bEEv16fuseml_gemm_desc"
 COPY = "__amd_rocclr_copyBuffer"
@@ -63,3 +63,35 @@ def test_traffic_scaled_by_copy_and_split_by_launch(tmp_path):
     k = {r["launch"]: r for r in t["kernels"]}
     assert abs(k[0]["fetch_bytes"] - 10.0 * 1024 * 1.25) < 1e-6 and abs(k[0]["write_bytes"] - 1.0 * 1024 * 1.25) < 1e-6
     assert abs(k[1]["fetch_bytes"] - 20.0 * 1024 * 1.25) < 1e-6 and abs(k[1]["write_bytes"] - 2.0 * 1024 * 1.25) < 1e-6
+
+
+def test_step_traffic_totals_every_kernel_per_call(tmp_path):
+    fields = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"]
+    copy_kib = 512 * 1024 / 2.0  # factor 2
+    rows = {"FETCH_SIZE": [], "WRITE_SIZE": []}
+    for c in rows:
+        rows[c].append({"Dispatch_Id": 1, "Kernel_Name": COPY, "Grid_Size": 512, "Counter_Name": c,
+                        "Counter_Value": copy_kib})
+    # three calls of a module with two kernels of different names (one launched twice per call)
+    d = 2
+    for _ in range(3):
+        for name, grid, f, w in [("Cijk_gemm", 1024, 100.0, 10.0), ("elementwise", 4096, 7.0, 7.0),
+                                 ("Cijk_gemm", 1024, 50.0, 5.0)]:
+            rows["FETCH_SIZE"].append({"Dispatch_Id": d, "Kernel_Name": name, "Grid_Size": grid,
+                                       "Counter_Name": "FETCH_SIZE", "Counter_Value": f})
+            rows["WRITE_SIZE"].append({"Dispatch_Id": d, "Kernel_Name": name, "Grid_Size": grid,
+                                       "Counter_Name": "WRITE_SIZE", "Counter_Value": w})
+            d += 1
+    # a one-off fill (fewer dispatches than calls) stays out of the per-call totals
+    for c in rows:
+        rows[c].append({"Dispatch_Id": d, "Kernel_Name": "fillBuffer", "Grid_Size": 64, "Counter_Name": c,
+                        "Counter_Value": 999.0})
+    pf, pw = tmp_path / "f.csv", tmp_path / "w.csv"
+    _write(pf, fields, rows["FETCH_SIZE"])
+    _write(pw, fields, rows["WRITE_SIZE"])
+    t = step_traffic(str(pf), str(pw), 512, calls=3)
+    assert abs(t["fetch_bytes_per_call"] - 157.0 * 1024 * 2) < 1e-6
+    assert abs(t["write_bytes_per_call"] - 22.0 * 1024 * 2) < 1e-6
+    k = {r["kernel"]: r for r in t["kernels"]}
+    assert not k["fillBuffer"]["per_call"] and k["elementwise"]["per_call"]
+    assert k["Cijk_gemm"]["dispatches"] == 6 and abs(k["Cijk_gemm"]["fetch_bytes_per_call"] - 150.0 * 2048) < 1e-6
