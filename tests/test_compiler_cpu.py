@@ -148,3 +148,23 @@ def test_cost_model_rules():
     gm3 = make_fx(f)(torch.randn(1024, 60, dtype=BF), torch.randn(60, 1024, dtype=BF))
     mm3 = [n for n in gm3.graph.nodes if n.op == "call_function"][0]
     assert trigger_is_fusible(mm3)[0] is False
+
+
+def test_cost_model_few_tiles_long_k():
+    """K >= 2048 with fewer 128x128 output tiles than CUs stays eager; a full
+    round of tiles, or a short K loop, is fused."""
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    def f(x, w):
+        return torch.mm(x, w)
+
+    def node(M, K, N):
+        gm = make_fx(f)(torch.randn(M, K, dtype=BF), torch.randn(K, N, dtype=BF))
+        return [n for n in gm.graph.nodes if n.op == "call_function"][0]
+
+    ok, why = trigger_is_fusible(node(1024, 2048, 1024))      # 8 x 8 = 64 tiles
+    assert ok is False and "64 output tiles at K=2048" in why
+    assert trigger_is_fusible(node(1024, 2048, 1024), min_tiles_long_k=0)[0]
+    assert trigger_is_fusible(node(2048, 2048, 2048))[0]       # 16 x 16 = 256 tiles
+    assert trigger_is_fusible(node(1024, 2040, 1024))[0]       # K < 2048
+    assert trigger_is_fusible(node(1024, 1024, 1024))[0]

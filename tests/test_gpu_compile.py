@@ -24,6 +24,10 @@ def _compile(model, **kw):
     from fuseml_amd.compiler import FuseMLCompiler
 
     torch._dynamo.reset()
+    # The workloads are scaled down (fewer output tiles than CUs at K >= 2048 for
+    # some GEMMs), where the cost model would route to eager: keep the fused
+    # kernels under test.
+    kw.setdefault("min_tiles_long_k", 0)
     be = FuseMLCompiler(**kw)
     return torch.compile(model, backend=be), be
 
@@ -38,6 +42,27 @@ def _close(got, ref, what):
     g = _f64(got)
     bad = ~np.isclose(g, ref, rtol=2e-2, atol=2e-2)
     assert not bad.any(), f"{what}: {bad.sum()} mismatches, max err {np.abs(g - ref).max()}"
+
+
+def test_few_tiles_long_k_is_routed_to_eager():
+    """Cost model on the device: Linear(2048 -> 1024) + GELU at M=1024 has 64
+    output tiles of 128x128 at K=2048, so the group runs eager; lowering the
+    tile floor fuses the same module, and both match eager."""
+    gen = torch.Generator().manual_seed(3)
+    lin = torch.nn.Linear(2048, 1024).to(torch.bfloat16)
+    m = torch.nn.Sequential(lin, torch.nn.GELU()).to("cuda")
+    x = torch.randn(1024, 2048, generator=gen).to(torch.bfloat16).to("cuda")
+    with torch.no_grad():
+        ref = m(x)
+        compiled, be = _compile(m, min_tiles_long_k=256)
+        out = compiled(x)
+    assert be.launchers == [] and be.fusion_applied is False
+    _close(out, _f64(ref), "eager-routed Linear+GELU")
+    with torch.no_grad():
+        compiled, be = _compile(m)
+        out = compiled(x)
+    assert be.fusion_applied and _launches(be) == 1
+    _close(out, _f64(ref), "fused Linear+GELU")
 
 
 def test_c1_fp32_small_is_bypassed():
