@@ -108,15 +108,31 @@ def _build_pipeline(name: str, wl, dev):
     return stages
 
 
-def _run_pipeline(stages, state, events=None):
+def _run_pipeline(stages, state, events=None, io=None):
     for i, (_, launcher, args, out_key, _) in enumerate(stages):
         if events is not None:
             events[i][0].record()
-        out = launcher(*args(state))
+        a = args(state)
+        out = launcher(*a)
         if events is not None:
             events[i][1].record()
+        if io is not None:
+            io.append((a, out))
         state[out_key] = out
     return state
+
+
+def _algorithmic_bytes(args, out):
+    """HBM bytes a launch must move at least: every distinct input tensor read
+    once (a [K,N] weight view counts its K*N elements) and every output written
+    once."""
+    seen, total = set(), 0
+    outs = out if isinstance(out, (tuple, list)) else (out,)
+    for t in list(args) + list(outs):
+        if isinstance(t, torch.Tensor) and (t.data_ptr(), t.numel()) not in seen:
+            seen.add((t.data_ptr(), t.numel()))
+            total += t.numel() * t.element_size()
+    return total
 
 
 def _initial_state(name, wl):
@@ -333,6 +349,14 @@ def main():
         flops = 2.0 * Mg * Ng * Kg
         per_kernel.append({"kernel": label, "avg_ms": round(avg, 4), "gemm_MNK": [Mg, Ng, Kg],
                            "tflops": round(flops / (avg * 1e-3) / 1e12, 1)})
+    # one more (untimed) pass to read each launch's operands and outputs
+    io = []
+    with torch.no_grad():
+        _run_pipeline(stages, dict(state), io=io)
+    torch.cuda.synchronize()
+    for pk, (a, out) in zip(per_kernel, io):
+        pk["algorithmic_bytes"] = _algorithmic_bytes(a, out)
+        pk["GBps"] = round(pk["algorithmic_bytes"] / (pk["avg_ms"] * 1e-3) / 1e9, 1)
     dom = max(range(len(per_kernel)), key=lambda i: per_kernel[i]["avg_ms"])
     dk = per_kernel[dom]
     Mg, Ng, Kg = dk["gemm_MNK"]
@@ -376,6 +400,11 @@ def main():
             "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": _traffic(name, dom),
         },
+        # the same dominant kernel against the HBM roofline: algorithmic bytes
+        # (inputs and outputs once) over its event-timed duration
+        "hbm_roofline": {"kernel": dk["kernel"], "algorithmic_bytes": dk["algorithmic_bytes"],
+                         "achieved": dk["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(dk["GBps"] / HBM_PEAK_GBS, 4)},
         "hbm_traffic": _hbm_traffic(name, wl.gemms),
         "cpu_baseline": cpu,
     }
