@@ -1,0 +1,45 @@
+"""CPU checks of bench.py's figures that do not need a GPU: algorithmic bytes
+per launch and the fused-against-eager traffic from the committed summaries."""
+
+import importlib.util
+import os
+
+import torch
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _bench():
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(REPO, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_algorithmic_bytes_counts_each_tensor_once():
+    b = _bench()
+    M, N, K = 64, 48, 32
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    w = torch.zeros(N, K, dtype=torch.bfloat16)
+    bias = torch.zeros(N, dtype=torch.bfloat16)
+    out = torch.zeros(M, N, dtype=torch.bfloat16)
+    # G2-style call: the residual is x itself, passed twice
+    got = b._algorithmic_bytes((bias, x, w.t(), x), out)
+    assert got == 2 * (N + M * K + N * K + M * N)
+    # tuple outputs (reductions in fp32 plus the tile)
+    red = torch.zeros(M, dtype=torch.float32)
+    assert b._algorithmic_bytes((x, w.t()), (red, red.clone(), out)) == 2 * (M * K + N * K + M * N) + 8 * M
+
+
+def test_hbm_traffic_from_committed_summaries():
+    b = _bench()
+    c2 = b._hbm_traffic("C2", [[16384, 4096, 1024], [16384, 1024, 4096]])
+    # the fused step writes exactly the two group outputs (h and y)
+    assert c2["fused_write_bytes"] == 16384 * 4096 * 2 + 16384 * 1024 * 2
+    assert c2["final_output_bytes"] == 16384 * 1024 * 2
+    assert 0.5 < c2["intermediate_eliminated_frac"] < 0.6
+    c3 = b._hbm_traffic("C3", [[16384, 4096, 1024]])
+    assert c3["intermediate_eliminated_frac"] == 1.0 and c3["saved_frac"] > 0.6
+    c5 = b._hbm_traffic("C5", [[8192, 16384, 4096], [8192, 4096, 16384]] * 4)
+    assert c5["fused_write_bytes"] == 4 * (8192 * 16384 * 2 + 8192 * 4096 * 2)
+    assert b._hbm_traffic("nope", [[1, 1, 1]]) is None
