@@ -3,9 +3,13 @@
 Replaces the reference's kernel cache (fuseml/codegen/kernel_cache.py:45-531:
 ``TensorFingerprint``, ``KernelCacheKey``, ``KernelCache``, ``build_cache_key``).
 Kernels are compiled ahead of time, so the cache only avoids rebuilding host
-launchers; the key is (op chain with the literal arguments that change the
-epilogue, per-input shape/stride/dtype fingerprints, output dtype, device
-arch).  Storage offsets and data alignment are checked per call by the C ABI,
+launchers; the key is (the group's derived :class:`EpilogueSpec` — op chain
+with operand positions and scalars, reductions, escape stores and the order of
+the returned values —, per-input shape/stride/dtype fingerprints, output
+shape and dtype, device arch).  Keying on the spec rather than on the node
+targets keeps two groups whose chains match but whose return signatures
+differ (e.g. the same reductions with and without the reduced value escaping)
+apart.  Storage offsets and data alignment are checked per call by the C ABI,
 so they need not be part of the key.
 """
 
@@ -19,7 +23,7 @@ import torch
 
 @dataclass(frozen=True)
 class LauncherCacheKey:
-    op_chain: Tuple[Tuple[str, Tuple[Any, ...]], ...]
+    spec: Any  # EpilogueSpec (frozen, hashable)
     inputs: Tuple[Tuple[Tuple[int, ...], Tuple[int, ...], str], ...]
     output: Tuple[Tuple[int, ...], str]
     arch: str
@@ -39,14 +43,6 @@ def _fingerprint(node: Any) -> Optional[Tuple[Tuple[int, ...], Tuple[int, ...], 
     return None
 
 
-def _literal(x: Any) -> Any:
-    if isinstance(x, torch.fx.Node):
-        return ("node",)
-    if isinstance(x, (list, tuple)):
-        return tuple(_literal(v) for v in x)
-    return x
-
-
 def _arch() -> str:
     if torch.cuda.is_available():
         try:
@@ -56,31 +52,20 @@ def _arch() -> str:
     return "cpu"
 
 
-def launcher_cache_key(group: Any) -> Optional[LauncherCacheKey]:
-    """Key of a group, or None when some metadata is missing or symbolic."""
-    chain = []
-    for n in group.all_nodes:
-        args = group.node_args_snapshot.get(n.name, n.args)
-        chain.append((str(n.target), _literal(tuple(args)) + tuple(sorted((k, _literal(v)) for k, v in n.kwargs.items()))))
-    # where each node's operands come from (input slot or group member) matters too
-    index = {id(x): i for i, x in enumerate(group.inputs)}
-    members = {id(x) for x in group.all_nodes}
-    wiring = []
-    for n in group.all_nodes:
-        args = group.node_args_snapshot.get(n.name, n.args)
-        wiring.append(tuple(("in", index[id(a)]) if id(a) in index else ("grp",) if id(a) in members else ("lit",)
-                            for a in args if isinstance(a, torch.fx.Node)))
+def launcher_cache_key(group: Any, spec: Any) -> Optional[LauncherCacheKey]:
+    """Key of a group whose spec is `spec`, or None when some metadata is
+    missing or symbolic."""
     fps = []
     for n in group.inputs:
         fp = _fingerprint(n)
         if fp is None:
             return None
         fps.append(fp)
-    out = group.output_metadata or {}
+    out = getattr(group, "output_metadata", None) or {}
     if "shape" not in out:
         return None
     return LauncherCacheKey(
-        op_chain=tuple(chain) + (("wiring", tuple(wiring)),),
+        spec=spec,
         inputs=tuple(fps),
         output=(tuple(int(s) for s in out["shape"]), str(out["dtype"])),
         arch=_arch(),

@@ -44,9 +44,9 @@ import torch.fx
 from torch._functorch.aot_autograd import aot_module_simplified, make_boxed_func
 
 from .cache import LauncherCache, launcher_cache_key
-from .epilogue import TRIGGER_TARGETS, UnsupportedGroup, spec_from_group
+from .epilogue import TRIGGER_TARGETS, EpilogueSpec, UnsupportedGroup, spec_from_group
 from .fusion_group import FusionGroup
-from .fusion_pass import FuseMLFusionPass, fuseml_fused_kernel_placeholder
+from .fusion_pass import FuseMLFusionPass, fuseml_fused_kernel_placeholder, group_eager_module
 
 logger = logging.getLogger("fuseml_amd")
 
@@ -107,29 +107,13 @@ def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSIO
     return True, "fused"
 
 
-def build_hip_launcher(group: FusionGroup, eager_fn: Optional[Callable[..., Any]] = None):
-    """FusionGroup -> HipKernelLauncher (eager fallback attached), or None.
+class EagerGroupLauncher:
+    """Callable that runs a group's original nodes (no fused kernel).
 
-    Replaces compiler.py:443-585 (``_build_launcher``) and 591-630
-    (``_build_cublas_launcher``): the epilogue spec is derived from the
-    group's nodes, arguments and kwargs; a group the kernel family cannot
-    express returns None and the caller installs the eager closure.
+    Bound where no kernel variant fits a group, with the launcher's calling
+    convention (``__name__``, positional ``*group.inputs``, the same return
+    structure), so that no raising placeholder is left in the graph.
     """
-    from .launcher import HipKernelLauncher
-
-    try:
-        spec = spec_from_group(group)
-    except UnsupportedGroup as exc:
-        logger.info("group %s stays eager: %s", group, exc)
-        return None
-    if eager_fn is None and group.eager_module is not None:
-        eager_fn = group.eager_module
-    return HipKernelLauncher(spec, len(group.inputs), eager_fn=eager_fn,
-                             kernel_signature=f"{group!r}: {spec.describe()}")
-
-
-class _EagerGroup:
-    """Callable running a group's original nodes (no fused kernel)."""
 
     def __init__(self, module: torch.fx.GraphModule) -> None:
         self.__name__ = "fuseml_eager_group"
@@ -137,6 +121,64 @@ class _EagerGroup:
 
     def __call__(self, *args):
         return self._module(*args)
+
+
+_EagerGroup = EagerGroupLauncher
+
+
+def group_eager_fn(group: Any) -> Optional[Callable[..., Any]]:
+    """The group's eager closure: this repository's ``eager_module`` if the
+    discovery pass set one, else one built from the reference's own fields
+    (a group formed by the reference's pass has no such field).  None when it
+    cannot be built."""
+    mod = getattr(group, "eager_module", None)
+    if mod is not None:
+        return mod
+    try:
+        return group_eager_module(group)
+    except Exception as exc:  # noqa: BLE001 - a malformed group must not abort compilation
+        logger.warning("no eager closure for %s: %s: %s", group, type(exc).__name__, exc)
+        return None
+
+
+def build_hip_launcher(group: Any, eager_fn: Optional[Callable[..., Any]] = None, *,
+                       spec: Optional[EpilogueSpec] = None, eager_if_unsupported: bool = True):
+    """FusionGroup -> launcher: replaces compiler.py:443-585 (``_build_launcher``)
+    and 591-630 (``_build_cublas_launcher``).
+
+    Accepts this repository's :class:`FusionGroup` and the reference's
+    (fuseml/fusion_group.py:74-85, any ``fusion_strategy``, with or without a
+    ``cublas_pattern``): only the reference's fields are read.  Returns
+
+    * a :class:`HipKernelLauncher` with the group's eager closure as its
+      fallback, when a kernel variant expresses the group;
+    * otherwise an :class:`EagerGroupLauncher` running the group's nodes
+      (``eager_if_unsupported``), so the caller never keeps the raising
+      placeholder;
+    * ``None`` only when neither can be built, or ``eager_if_unsupported`` is
+      False and no variant fits.
+
+    Never raises for a group it cannot express (``AttributeError`` and the like
+    from an unexpected group become the eager path).  A missing HIP library
+    raises ``ImportError``: the product path does not fall back silently.
+    """
+    from .launcher import HipKernelLauncher
+
+    if eager_fn is None:
+        eager_fn = group_eager_fn(group)
+    if spec is None:
+        try:
+            spec = spec_from_group(group)
+        except UnsupportedGroup as exc:
+            logger.info("group %s stays eager: %s", group, exc)
+        except Exception as exc:  # noqa: BLE001
+            logger.warning("group %s stays eager: %s: %s", group, type(exc).__name__, exc)
+    if spec is None:
+        if eager_if_unsupported and eager_fn is not None:
+            return EagerGroupLauncher(eager_fn)
+        return None
+    return HipKernelLauncher(spec, len(group.inputs), eager_fn=eager_fn,
+                             kernel_signature=f"{group!r}: {spec.describe()}")
 
 
 class FuseMLCompiler:
@@ -214,14 +256,21 @@ class FuseMLCompiler:
             ok = group.base_node.meta.get("fuseml_cost_model") == "fused"
             launcher = None
             if ok:
-                key = launcher_cache_key(group)
+                try:
+                    spec = spec_from_group(group)
+                except UnsupportedGroup as exc:
+                    logger.info("group %s stays eager: %s", group, exc)
+                    spec = None
+                key = launcher_cache_key(group, spec) if spec is not None else None
                 launcher = self._cache.lookup(key) if key is not None else None
-                if launcher is None:
+                if launcher is None and spec is not None:
                     launcher = build_hip_launcher(group)
+                    if isinstance(launcher, EagerGroupLauncher):
+                        launcher = None
                     if launcher is not None and key is not None:
                         self._cache.store(key, launcher)
             if launcher is None:
-                target: Callable = _EagerGroup(group.eager_module)
+                target: Callable = EagerGroupLauncher(group.eager_module)
                 strategies.add("eager")
             else:
                 target = launcher

@@ -159,16 +159,129 @@ def _group_args(group: Any, node: torch.fx.Node) -> tuple:
     return tuple(snap.get(node.name, node.args))
 
 
+def group_nodes(group: Any) -> List[Any]:
+    """``base_node`` followed by ``fused_nodes`` (the reference's ``all_nodes``)."""
+    return [group.base_node, *group.fused_nodes]
+
+
+def input_slots(group: Any) -> Tuple[Dict[int, int], Dict[int, Any]]:
+    """Launcher position of every external node the group's nodes consume.
+
+    Returns ``(slots, via_view)``.  ``slots`` maps ``id(node)``, for each node
+    that the argument snapshot names outside the group, to its index in
+    ``group.inputs``.  ``via_view`` holds the operands that reach the group
+    through a transparent view op: the launcher receives the view's source,
+    not the view.
+
+    Groups formed by this repository's pass name their inputs directly.  A
+    group from the reference's own pass can differ in two ways, both handled
+    by position (the reference collects inputs in first-appearance order over
+    each node's args, fuseml/passes/fusion_pass.py:500-535):
+
+    * its surgery patches ``inputs`` to the replacement of an earlier group's
+      output but not ``node_args_snapshot`` (fusion_pass.py:716-727), so the
+      snapshot still names the erased node;
+    * it resolves an argument through transparent view ops to the defining
+      node (fuseml/passes/topology.py:198-226).
+    Raises :class:`UnsupportedGroup` when the two lists do not line up.
+    """
+    inputs = list(group.inputs)
+    members = {id(n) for n in group_nodes(group)}
+    ordered: List[Any] = []
+    seen = set()
+    for n in group_nodes(group):
+        for a in _group_args(group, n):
+            if _is_node(a) and id(a) not in members and id(a) not in seen:
+                seen.add(id(a))
+                ordered.append(a)
+    direct = {id(n): i for i, n in enumerate(inputs)}
+    if all(id(a) in direct for a in ordered):
+        return {id(a): direct[id(a)] for a in ordered}, {}
+    if len(ordered) != len(inputs):
+        raise UnsupportedGroup(
+            f"{len(inputs)} group inputs do not line up with the {len(ordered)} external arguments")
+    slots: Dict[int, int] = {}
+    via_view: Dict[int, Any] = {}
+    for i, a in enumerate(ordered):
+        if id(a) in direct and direct[id(a)] != i:
+            raise UnsupportedGroup(f"input {a.name} is at position {direct[id(a)]}, expected {i}")
+        slots[id(a)] = i
+        if a is not inputs[i] and getattr(a, "op", None) == "call_function" and a.target in TRANSPARENT_TARGETS:
+            via_view[id(a)] = a
+    return slots, via_view
+
+
+def reduction_dims(node: Any, args: Optional[tuple] = None) -> Any:
+    """The ``dim`` argument of a sum.dim_IntList / amax / mean.dim node (None if absent)."""
+    args = tuple(node.args) if args is None else tuple(args)
+    if len(args) > 1:
+        return args[1]
+    return node.kwargs.get("dim")
+
+
+def is_full_reduction(dims: Any) -> bool:
+    """``dim`` None or empty: the op reduces over every element (a 0-d result).
+
+    That is the meaning of an omitted or empty ``dim`` for ``amax`` and of
+    ``dim=None`` / ``dim=[]`` for ``sum.dim_IntList`` and ``mean.dim``.  Such a
+    reduction is not a row or column reduction of the tile.
+    """
+    if dims is None:
+        return True
+    return isinstance(dims, (list, tuple)) and len(dims) == 0
+
+
+def transparent_is_identity(node: Any, args: Optional[tuple] = None) -> bool:
+    """A shape-preserving transparent op that also keeps the element order.
+
+    A ``permute`` with non-identity dims on a square value keeps the shape but
+    transposes the data (the reference treats every shape-preserving
+    transparent op as a no-op, fuseml/passes/topology.py:84-96, and would
+    drop the transpose).  Strides are compared too when both nodes carry them.
+    """
+    args = tuple(node.args) if args is None else tuple(args)
+    if node.target is aten.permute.default:
+        dims = args[1] if len(args) > 1 else node.kwargs.get("dims")
+        if dims is None:
+            return False
+        nd = len(dims)
+        if [int(d) % nd for d in dims] != list(range(nd)):
+            return False
+    src = args[0] if args else None
+    a, b = _node_stride(src), _node_stride(node)
+    if a is not None and b is not None and a != b:
+        return False
+    return True
+
+
+def _node_stride(node: Any) -> Optional[Tuple[int, ...]]:
+    meta = getattr(node, "meta", {}) or {}
+    tm = meta.get("tensor_meta")
+    if tm is not None and hasattr(tm, "stride"):
+        try:
+            return tuple(int(s) for s in tm.stride)
+        except (TypeError, ValueError):
+            return None
+    val = meta.get("val")
+    if val is not None and hasattr(val, "stride"):
+        try:
+            return tuple(int(s) for s in val.stride())
+        except (TypeError, ValueError):
+            return None
+    return None
+
+
 def reduction_axis(dims: Any, ndim: int = 2) -> int:
     """Map reduction dims of a 2-D [M,N] value to a tile axis.
 
     Follows fuseml/codegen/kernel_generator.py:1909-1931: dims are normalised
     modulo 2; any 1 means "reduce along N" (axis 1, result [M]); otherwise axis 0.
     An N-D value ([*lead, N], ndim > 2) supports only the last dimension
-    (axis 1, result [*lead]).
+    (axis 1, result [*lead]).  ``dim`` None or empty reduces over every
+    element (a 0-d result), which is no tile axis: :class:`UnsupportedGroup`.
     """
-    if dims is None:
-        dims = [-1]
+    if is_full_reduction(dims):
+        raise UnsupportedGroup("a reduction over all elements is not a row/column reduction")
     if isinstance(dims, int):
         dims = [dims]
     if ndim > 2:
@@ -188,8 +301,7 @@ def spec_from_group(group: Any) -> EpilogueSpec:
     base = group.base_node
     if base.target not in TRIGGER_TARGETS:
         raise UnsupportedGroup(f"base node {base.target} is not addmm/mm")
-    inputs = list(group.inputs)
-    index = {id(n): i for i, n in enumerate(inputs)}
+    index, via_view = input_slots(group)
     members = {id(n) for n in [base, *group.fused_nodes]}
     escapes = list(getattr(group, "intermediate_outputs", []) or [])
     escape_idx = {id(n): k for k, n in enumerate(escapes)}
@@ -197,6 +309,8 @@ def spec_from_group(group: Any) -> EpilogueSpec:
     def input_index(n: Any) -> int:
         if not _is_node(n) or id(n) not in index:
             raise UnsupportedGroup(f"operand {n!r} is not a group input")
+        if id(n) in via_view:
+            raise UnsupportedGroup(f"operand {n.name} reaches the group through a view of another input")
         return index[id(n)]
 
     ops: List[EpiOp] = []
@@ -249,8 +363,7 @@ def spec_from_group(group: Any) -> EpilogueSpec:
             keepdim = bool(args[2]) if len(args) > 2 else bool(node.kwargs.get("keepdim", False))
             if keepdim:
                 raise UnsupportedGroup("keepdim=True reductions are not fused")
-            ax = reduction_axis(args[1] if len(args) > 1 else node.kwargs.get("dim"),
-                                len(cur_shape) if cur_shape else 2)
+            ax = reduction_axis(reduction_dims(node, args), len(cur_shape) if cur_shape else 2)
             if red_axis is not None and ax != red_axis:
                 raise UnsupportedGroup("sibling reductions along different axes")
             red_axis = ax
@@ -261,7 +374,11 @@ def spec_from_group(group: Any) -> EpilogueSpec:
             raise UnsupportedGroup("op after a reduction")
         if t in TRANSPARENT_TARGETS:
             new_shape = _node_shape(node)
+            if new_shape == cur_shape and not transparent_is_identity(node, args):
+                raise UnsupportedGroup(f"{node.name}: {t} keeps the shape but reorders the elements")
             if new_shape != cur_shape:
+                if t is aten.permute.default:
+                    raise UnsupportedGroup(f"{node.name}: permute changes the layout")
                 if not leading_dim_view(cur_shape, new_shape):
                     raise UnsupportedGroup(f"{node.name}: view changes more than the row dimension")
                 cur_shape = new_shape

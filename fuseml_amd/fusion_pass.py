@@ -55,7 +55,14 @@ from .epilogue import (
     TRANSPARENT_TARGETS,
     TRIGGER_TARGETS,
     UNARY_TARGETS,
+    UnsupportedGroup,
+    _group_args,
+    group_nodes,
+    input_slots,
+    is_full_reduction,
     leading_dim_view,
+    reduction_dims,
+    transparent_is_identity,
 )
 from .fusion_group import FusionGroup
 
@@ -76,6 +83,72 @@ def fuseml_fused_kernel_placeholder(*args):
     raise RuntimeError(
         "fuseml_fused_kernel_placeholder must be replaced by a fused launcher before execution"
     )
+
+
+def group_result_nodes(group: Any) -> List[torch.fx.Node]:
+    """Nodes whose values a fused call returns, in return order: the output
+    node, any sibling reductions, then the escapes (the order of the surgery's
+    ``getitem`` indices, fuseml/passes/fusion_pass.py:824-880)."""
+    return [group.output_node, *(getattr(group, "sibling_outputs", None) or []),
+            *(getattr(group, "intermediate_outputs", None) or [])]
+
+
+def group_eager_module(group: Any) -> torch.fx.GraphModule:
+    """The group's own nodes as a standalone GraphModule: ``*group.inputs -> results``.
+
+    Built only from the reference's ``FusionGroup`` fields (fuseml/fusion_group.py:74-85):
+    ``inputs``, ``base_node``/``fused_nodes`` with their targets and kwargs,
+    ``node_args_snapshot`` for their args (surgery erases the nodes and FX
+    nulls their Node arguments, fusion_pass.py:342-343), ``output_node`` and
+    ``intermediate_outputs``.  It is the eager fallback of a fused launch and
+    the callable bound when no kernel variant fits, so no raising placeholder
+    is ever left in the graph (the reference's compiler keeps one,
+    fuseml/compiler.py:393-398).  An operand that the reference resolved
+    through view ops to their source is re-viewed here from the live view
+    nodes; raises :class:`UnsupportedGroup` if those are gone.
+    """
+    slots, via_view = input_slots(group)
+    g = torch.fx.Graph()
+    inputs = list(group.inputs)
+    ph = [g.placeholder(f"in{i}") for i in range(len(inputs))]
+    env: Dict[int, torch.fx.Node] = {}
+
+    def external(a: torch.fx.Node) -> torch.fx.Node:
+        if id(a) in env:
+            return env[id(a)]
+        slot = slots[id(a)]
+        val = ph[slot]
+        if id(a) in via_view:
+            chain = []
+            cur = a
+            while cur is not inputs[slot]:
+                if (getattr(cur, "op", None) != "call_function" or cur.target not in TRANSPARENT_TARGETS
+                        or not cur.args or not isinstance(cur.args[0], torch.fx.Node)):
+                    raise UnsupportedGroup(f"view chain from {inputs[slot]} to {a.name} is not available")
+                chain.append(cur)
+                cur = cur.args[0]
+            for v in reversed(chain):
+                val = g.call_function(v.target, (val, *v.args[1:]), dict(v.kwargs))
+        env[id(a)] = val
+        return val
+
+    members = {id(n) for n in group_nodes(group)}
+
+    def arg(a: Any) -> Any:
+        if isinstance(a, torch.fx.Node):
+            return env[id(a)] if id(a) in members else external(a)
+        if isinstance(a, (list, tuple)):
+            return type(a)(arg(x) for x in a)
+        return a
+
+    for n in group_nodes(group):
+        args = tuple(arg(a) for a in _group_args(group, n))
+        if any(isinstance(v, torch.fx.Node) for v in n.kwargs.values()):
+            raise UnsupportedGroup(f"{n.name}: a tensor keyword argument is not part of the group's inputs")
+        env[id(n)] = g.call_function(n.target, args, dict(n.kwargs))
+    res = [env[id(n)] for n in group_result_nodes(group)]
+    g.output(res[0] if len(res) == 1 else tuple(res))
+    return torch.fx.GraphModule(torch.nn.Module(), g)
 
 
 def _meta_shape(node: Any):
@@ -107,10 +180,20 @@ def _keepdim(node: torch.fx.Node) -> bool:
 
 
 def _red_dims(node: torch.fx.Node):
-    dims = node.args[1] if len(node.args) > 1 else node.kwargs.get("dim")
-    if dims is None:
+    dims = reduction_dims(node)
+    if is_full_reduction(dims):
         return None
     return tuple(int(d) % 2 for d in (dims if isinstance(dims, (list, tuple)) else [dims]))
+
+
+def _fusible_reduction(node: torch.fx.Node) -> bool:
+    """A row/column reduction the kernel can take: keepdim=False and a ``dim``.
+
+    A reduction with ``dim`` omitted, None or empty reduces every element to a
+    0-d result; it stays outside the group (the reference absorbs it and its
+    kernel reduces along one axis only, kernel_generator.py:1909-1931).
+    """
+    return not _keepdim(node) and not is_full_reduction(reduction_dims(node))
 
 
 class FuseMLFusionPass:
@@ -142,9 +225,16 @@ class FuseMLFusionPass:
     # ------------------------------------------------------------------
     @staticmethod
     def _shape_preserving_2d(node: torch.fx.Node) -> bool:
+        """A 2-D view op that changes neither the shape nor the element order.
+
+        The reference absorbs any shape-preserving transparent op
+        (fusion_pass.py:537-579); a non-identity ``permute`` of a square value
+        keeps the shape but transposes it, so it is not absorbed here.
+        """
         src = node.args[0] if node.args else None
         a, b = _meta_shape(src), _meta_shape(node)
-        return a is not None and b is not None and len(a) == 2 and a == b
+        return (a is not None and b is not None and len(a) == 2 and a == b
+                and transparent_is_identity(node))
 
     _LEADING_VIEW_TARGETS = (aten.view.default, aten._unsafe_view.default, aten.reshape.default)
 
@@ -160,7 +250,7 @@ class FuseMLFusionPass:
             return False
         u = users[0]
         if u.target in REDUCTION_TARGETS:
-            return not _keepdim(u)
+            return _fusible_reduction(u)
         if u.target in INPLACE_TARGETS:
             return bool(u.args) and u.args[0] is node
         return u.target in POINTWISE_TARGETS
@@ -170,8 +260,10 @@ class FuseMLFusionPass:
         reds = [u for u in node.users if u.op == "call_function" and u.target in REDUCTION_TARGETS]
         if len(reds) < 1:
             return []
+        if not all(_fusible_reduction(u) for u in reds):
+            return []
         axes = {_red_dims(u) for u in reds}
-        if len(axes) != 1 or any(_keepdim(u) for u in reds):
+        if len(axes) != 1:
             return []
         kinds = [REDUCTION_TARGETS[u.target] for u in reds]
         if len(set(kinds)) != len(kinds):
@@ -221,7 +313,7 @@ class FuseMLFusionPass:
                     break
                 t = nxt.target
                 if t in REDUCTION_TARGETS:
-                    if _keepdim(nxt):
+                    if not _fusible_reduction(nxt):
                         break
                     absorb(nxt)
                     break
@@ -259,7 +351,7 @@ class FuseMLFusionPass:
                 for n in group.all_nodes:
                     group.node_args_snapshot[n.name] = tuple(n.args)
                 self._resolve_params(group)
-                group.eager_module = self._eager_module(group)
+                group.eager_module = group_eager_module(group)
                 groups.append(group)
         return groups
 
@@ -288,18 +380,6 @@ class FuseMLFusionPass:
                     continue
                 if isinstance(obj, torch.Tensor):
                     group.param_bindings[str(n.target)] = obj
-
-    def _eager_module(self, group: FusionGroup) -> torch.fx.GraphModule:
-        """The group's own nodes as a GraphModule: inputs -> result tuple."""
-        g = torch.fx.Graph()
-        env: Dict[torch.fx.Node, torch.fx.Node] = {}
-        for i, n in enumerate(group.inputs):
-            env[n] = g.placeholder(f"in{i}")
-        for n in group.all_nodes:
-            env[n] = g.node_copy(n, lambda a: env[a])
-        res = [env[n] for n in group.result_nodes]
-        g.output(res[0] if len(res) == 1 else tuple(res))
-        return torch.fx.GraphModule(self.graph_module, g)
 
     # ------------------------------------------------------------------
     def _apply_surgery(self, groups: List[FusionGroup]) -> None:

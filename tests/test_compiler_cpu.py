@@ -13,6 +13,7 @@
 import pytest
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 import fuseml_amd.compiler as comp
 from fuseml_amd.compiler import FuseMLCompiler, trigger_is_fusible
@@ -168,3 +169,34 @@ def test_cost_model_few_tiles_long_k():
     assert trigger_is_fusible(node(2048, 2048, 2048))[0]       # 16 x 16 = 256 tiles
     assert trigger_is_fusible(node(1024, 2040, 1024))[0]       # K < 2048
     assert trigger_is_fusible(node(1024, 1024, 1024))[0]
+
+
+class _TwoReductionChains(nn.Module):
+    """Two mm -> gelu -> {sum, amax} chains of equal shapes; in the second the
+    GELU value is also returned, so its group returns (sum, amax, tile)."""
+
+    def __init__(self):
+        super().__init__()
+        self.a = nn.Linear(64, 128, bias=False)
+        self.b = nn.Linear(64, 128, bias=False)
+
+    def forward(self, x):
+        h1 = F.gelu(self.a(x))
+        h2 = F.gelu(self.b(x))
+        return h1.sum(-1), h1.amax(-1), h2.sum(-1), h2.amax(-1), h2
+
+
+def test_cache_key_separates_return_signatures(recorded):
+    torch.manual_seed(0)
+    m = _TwoReductionChains().to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0, fuse_sibling_reductions=True)
+    with torch.no_grad():
+        got = _compile(m, be)(x)
+        ref = m(x)
+    for a, b in zip(got, ref):
+        assert a.shape == b.shape and torch.allclose(a.float(), b.float(), atol=1e-2)
+    assert (be.cache.misses, be.cache.hits) == (2, 0)
+    outs = sorted(r.spec.outputs for r in recorded.built)
+    assert outs == sorted([(("red", "sum"), ("red", "amax")),
+                           (("red", "sum"), ("red", "amax"), ("tile",))])

@@ -275,3 +275,69 @@ def test_leading_dim_view_rule():
     assert not leading_dim_view((16, 64), (16, 8, 8))     # splits N
     assert not leading_dim_view((16, 64), (2, 512))       # moves elements across rows
     assert not leading_dim_view((16, 64), (64,))
+
+
+def test_square_permute_is_not_absorbed():
+    """relu((x @ w).T) on a square output: the permute keeps the shape but
+    transposes, so it ends the group (mm alone is no group) and the graph
+    still computes the transpose."""
+    def f(x, w):
+        return torch.relu((x @ w).T)
+
+    x, w = torch.randn(64, 32), torch.randn(32, 64)
+    p, gm = run_pass(f, (x, w))
+    assert all(aten.permute.default not in targets(g) for g in p.groups)
+    bind_eager(gm, p.groups)
+    assert torch.equal(gm(x, w), f(x, w))
+
+
+def test_identity_permute_is_absorbed_as_noop():
+    def f(x, w):
+        return torch.relu((x @ w).permute(0, 1))
+
+    x, w = torch.randn(64, 32), torch.randn(32, 64)
+    p, gm = run_pass(f, (x, w))
+    (g,) = p.groups
+    assert targets(g) == [aten.mm.default, aten.permute.default, aten.relu.default]
+    assert spec_from_group(g).describe() == "gemm(0,1) -> relu"
+
+
+@pytest.mark.parametrize("red", ["amax_all", "sum_empty", "mean_none"])
+def test_full_reduction_is_not_absorbed(red):
+    """A reduction with no dim (or an empty one) reduces every element to a
+    0-d value: it stays outside the group, which keeps mm -> relu."""
+    def f(x, w):
+        h = torch.relu(x @ w)
+        if red == "amax_all":
+            return torch.amax(h)
+        if red == "sum_empty":
+            return torch.sum(h, dim=[])
+        return torch.mean(h, dim=None)
+
+    x, w = torch.randn(16, 32), torch.randn(32, 24)
+    p, gm = run_pass(f, (x, w))
+    (g,) = p.groups
+    assert targets(g) == [aten.mm.default, aten.relu.default]
+    bind_eager(gm, p.groups)
+    out = gm(x, w)
+    assert out.shape == () and torch.allclose(out, f(x, w))
+
+
+def test_full_reduction_siblings_are_not_absorbed():
+    def f(x, w):
+        h = torch.relu(x @ w)
+        return h.sum(-1), torch.amax(h), h.mean(-1)
+
+    x, w = torch.randn(16, 32), torch.randn(32, 24)
+    p, gm = run_pass(f, (x, w), fuse_sibling_reductions=True)
+    (g,) = p.groups
+    assert targets(g) == [aten.mm.default, aten.relu.default]
+
+
+def test_reduction_axis_rejects_full_reductions():
+    from fuseml_amd.epilogue import UnsupportedGroup, reduction_axis
+
+    for dims in (None, [], ()):
+        with pytest.raises(UnsupportedGroup):
+            reduction_axis(dims)
+    assert reduction_axis([-1]) == 1 and reduction_axis(0) == 0

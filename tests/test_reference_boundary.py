@@ -1,0 +1,213 @@
+"""The drop-in boundary with the reference's own FusionGroup (CPU, no kernel launch).
+
+INTEGRATION route B: the reference keeps its compiler, discovery and surgery
+and calls ``build_hip_launcher(group)`` where it built a Triton or cuBLASLt
+launcher (fuseml/compiler.py:343-409).  The groups it hands over carry only
+the ten fields of fuseml/fusion_group.py:74-85, their nodes are erased by the
+time the launcher is built, and later groups' ``node_args_snapshot`` still
+names the erased output of an earlier group.  These tests form such groups
+(``refsurgery``), bind what ``build_hip_launcher`` returns in place of each
+placeholder, and run the graph: the fused launches are forced onto their
+eager fallback (``FUSEML_HIP_FORCE_FAIL``) so the whole route runs on the CPU
+and is compared with the eager module.
+"""
+
+import dataclasses
+
+import pytest
+import torch
+import torch.nn as nn
+from torch.fx.experimental.proxy_tensor import make_fx
+
+from fuseml_amd.compiler import EagerGroupLauncher, build_hip_launcher
+from fuseml_amd.epilogue import spec_from_group
+from fuseml_amd.fallback import FORCE_FAIL_ENV
+from fuseml_amd.launcher import HipKernelLauncher
+from fuseml_amd.workloads import ActivationHeavy, StackedMLP, TransformerMLP
+from refsurgery import RefGroup, bind, reference_groups, reference_surgery
+
+BF = torch.bfloat16
+REFERENCE_FIELDS = ["base_node", "fused_nodes", "inputs", "output_node", "output_metadata",
+                    "intermediate_outputs", "param_bindings", "node_args_snapshot",
+                    "fusion_strategy", "cublas_pattern"]
+
+
+def trace(model, *inputs):
+    with torch.no_grad():
+        return make_fx(model)(*inputs)
+
+
+def route_b(model, inputs, cublas=False):
+    gm = trace(model, *inputs)
+    groups = reference_groups(gm, inputs, cublas=cublas)
+    phs = reference_surgery(gm, groups)
+    bound = bind(gm, phs, build_hip_launcher)
+    return gm, groups, bound
+
+
+def test_refgroup_has_exactly_the_reference_fields():
+    assert [f.name for f in dataclasses.fields(RefGroup)] == REFERENCE_FIELDS
+
+
+@pytest.mark.parametrize("cublas", [False, True], ids=["triton", "cublas_epilogue"])
+def test_route_b_mlp_block(monkeypatch, cublas):
+    torch.manual_seed(0)
+    m = TransformerMLP(64, 256).to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    gm, groups, bound = route_b(m, (x,), cublas=cublas)
+    assert all(isinstance(b, HipKernelLauncher) for b in bound)
+    assert [b.spec.describe() for b in bound] == ["gemm(1,2) -> add[0] -> gelu_erf",
+                                                  "gemm(1,2) -> add[0] -> add[3]"]
+    if cublas:
+        assert groups[0].fusion_strategy == "cublas_epilogue"
+        assert groups[0].cublas_pattern.epilogue_type == "GELU_BIAS"
+    # GEMM2's snapshot still names the erased GELU node; its input is the replacement
+    g2 = groups[1]
+    stale = g2.node_args_snapshot[g2.base_node.name][1]
+    assert stale is not g2.inputs[1] and stale.name.startswith("gelu")
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    with torch.no_grad():
+        out = gm(x)
+        ref = m(x)
+    assert torch.equal(out, ref)
+    assert [b.fallback_count for b in bound] == [1, 1]
+
+
+def test_route_b_stacked_blocks(monkeypatch):
+    torch.manual_seed(1)
+    m = StackedMLP(64, 128, 3).to(BF).eval()
+    x = torch.randn(16, 64, dtype=BF)
+    gm, groups, bound = route_b(m, (x,))
+    assert len(bound) == 6 and all(isinstance(b, HipKernelLauncher) for b in bound)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    with torch.no_grad():
+        assert torch.equal(gm(x), m(x))
+
+
+def test_route_b_activation_heavy_role_bias(monkeypatch):
+    torch.manual_seed(0)
+    m = ActivationHeavy(64, 128).to(BF).eval()
+    with torch.no_grad():
+        m.row.uniform_(-0.5, 0.5)
+    x, g = torch.randn(32, 64, dtype=BF), torch.rand(32, 128, dtype=BF)
+    gm, groups, bound = route_b(m, (x, g))
+    (b,) = bound
+    assert b.spec.describe() == "gemm(1,2) -> add[0] -> relu -> mul[3] -> sigmoid -> add[4]"
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    with torch.no_grad():
+        assert torch.equal(gm(x, g), m(x, g))
+
+
+def _absorb(gm, group, node):
+    """Extend a RefGroup the way the reference's absorption would (its rules
+    take a full reduction, fusion_pass.py:223-241, and a shape-preserving
+    permute, fusion_pass.py:537-579)."""
+    group.fused_nodes.append(node)
+    group.output_node = node
+    group.node_args_snapshot[node.name] = tuple(node.args)
+
+
+def test_route_b_escape_returns_tuple(monkeypatch):
+    """A group whose middle node is also used outside (the reference's escape
+    analysis, fusion_pass.py:300-329): the launcher returns (primary, escape)."""
+    def f(x, w):
+        h = torch.relu(x @ w)
+        return torch.sigmoid(h) * 2.0, h
+
+    x, w = torch.randn(32, 64, dtype=BF), torch.randn(64, 96, dtype=BF)
+    gm = trace(f, x, w)
+    torch.fx.passes.shape_prop.ShapeProp(gm).propagate(x, w)
+    nodes = {n.target: n for n in gm.graph.nodes if n.op == "call_function"}
+    mm = nodes[torch.ops.aten.mm.default]
+    g = RefGroup(base_node=mm, inputs=list(mm.args), output_node=mm,
+                 node_args_snapshot={mm.name: tuple(mm.args)})
+    for t in (torch.ops.aten.relu.default, torch.ops.aten.sigmoid.default, torch.ops.aten.mul.Tensor):
+        _absorb(gm, g, nodes[t])
+    g.intermediate_outputs = [nodes[torch.ops.aten.relu.default]]
+    g.output_metadata = {"shape": (32, 96), "stride": (96, 1), "dtype": BF}
+    phs = reference_surgery(gm, [g])
+    (b,) = bind(gm, phs, build_hip_launcher)
+    assert isinstance(b, HipKernelLauncher)
+    assert b.spec.outputs == (("tile",), ("extra", 0))
+    assert b.spec.describe() == "gemm(0,1) -> relu -> store[0] -> sigmoid -> scale"
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    with torch.no_grad():
+        y, h = gm(x, w)
+        ry, rh = f(x, w)
+    assert torch.equal(y, ry) and torch.equal(h, rh)
+
+
+def test_route_b_full_reduction_gets_eager_closure():
+    """torch.amax(relu(x @ w)): a reduction over every element is no tile axis.
+    The reference fuses it as a per-row amax; here the group is bound to its
+    eager nodes and the 0-d result is right."""
+    def f(x, w):
+        return torch.amax(torch.relu(x @ w))
+
+    x, w = torch.randn(32, 64, dtype=BF), torch.randn(64, 48, dtype=BF)
+    gm = trace(f, x, w)
+    (g,) = reference_groups(gm, (x, w))
+    amax = [n for n in gm.graph.nodes if n.target is torch.ops.aten.amax.default][0]
+    assert amax not in g.fused_nodes  # this repository's discovery leaves it out
+    _absorb(gm, g, amax)
+    phs = reference_surgery(gm, [g])
+    (b,) = bind(gm, phs, build_hip_launcher)
+    assert isinstance(b, EagerGroupLauncher)
+    with torch.no_grad():
+        out = gm(x, w)
+    assert out.shape == () and torch.equal(out, f(x, w))
+
+
+def test_route_b_square_permute_gets_eager_closure():
+    def f(x, w):
+        return torch.relu((x @ w).T)
+
+    x, w = torch.randn(64, 32, dtype=BF), torch.randn(32, 64, dtype=BF)
+    gm = trace(f, x, w)
+    nodes = {n.target: n for n in gm.graph.nodes if n.op == "call_function"}
+    mm, perm, relu = (nodes[torch.ops.aten.mm.default], nodes[torch.ops.aten.permute.default],
+                      nodes[torch.ops.aten.relu.default])
+    torch.fx.passes.shape_prop.ShapeProp(gm).propagate(x, w)
+    g = RefGroup(base_node=mm, inputs=list(mm.args), output_node=mm,
+                 node_args_snapshot={mm.name: tuple(mm.args)})
+    _absorb(gm, g, perm)
+    _absorb(gm, g, relu)
+    g.output_metadata = {"shape": (64, 64), "stride": (64, 1), "dtype": BF}
+    phs = reference_surgery(gm, [g])
+    (b,) = bind(gm, phs, build_hip_launcher)
+    assert isinstance(b, EagerGroupLauncher)
+    with torch.no_grad():
+        assert torch.equal(gm(x, w), f(x, w))
+
+
+def test_malformed_group_is_not_an_attribute_error():
+    """A group object missing fields makes the builder return None (the caller
+    keeps its own path); it does not raise AttributeError out of compilation."""
+    class Bare:
+        def __init__(self, base):
+            self.base_node = base
+            self.fused_nodes = []
+            self.inputs = []
+
+        def __repr__(self):
+            return "Bare()"
+
+    def f(x, w):
+        return torch.relu(x @ w)
+
+    gm = trace(f, torch.randn(8, 8, dtype=BF), torch.randn(8, 8, dtype=BF))
+    mm = [n for n in gm.graph.nodes if n.target is torch.ops.aten.mm.default][0]
+    assert build_hip_launcher(Bare(mm)) is None
+
+
+def test_spec_from_reference_group_uses_input_positions():
+    torch.manual_seed(0)
+    m = TransformerMLP(64, 256).to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    gm = trace(m, x)
+    groups = reference_groups(gm, (x,))
+    reference_surgery(gm, groups)
+    specs = [spec_from_group(g) for g in groups]
+    # GEMM2: inputs (b2, <replacement of GELU>, t(W2), x) -> left operand slot 1, residual slot 3
+    assert (specs[1].left, specs[1].right) == (1, 2)
+    assert specs[1].ops[-1].operand == 3
