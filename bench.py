@@ -1,24 +1,34 @@
-"""Benchmark of the fused MLP-block hot path on one MI355X.
+"""Benchmark of the fused GEMM+epilogue hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2|C3|C4|C5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2]
+                    [--configs C2,C3,C4,C5] [--no-cpu] [--no-eager] [--no-compile]
 
-A step is one forward of the workload through the fused HIP kernels (for the
-default C2 MLP block: GEMM1+bias+GELU and GEMM2+bias+residual, two launches of
-the gfx950 kernel family through the C ABI), on synthetic seeded inputs that are
-resident in HBM before timing starts.  W untimed steps, then K timed steps
-bracketed by ``torch.cuda.synchronize()``.  Rank 0 prints one JSON line:
+Headline (the driver's contract).  A step is one forward of the headline
+workload (default C2, the MLP block: GEMM1+bias+GELU and GEMM2+bias+residual,
+two launches of the gfx950 kernel family through the C ABI) on synthetic
+seeded inputs resident in HBM.  W untimed steps, then exactly K timed steps
+bracketed by ``torch.cuda.synchronize()``; ``value`` = wall ms per step.
+Rank 0 prints one JSON line carrying:
 
-* ``value``/``ms_per_step`` — fused block latency in ms (lower is better);
-* ``roofline`` — the dominant kernel's algorithmic FLOPs per launch divided by
-  its average launch duration, measured with HIP events on the launch stream
-  inside the timed region, against the bf16 dense MFMA peak (every config is
-  MFMA-bound on MI355X: arithmetic intensity 443-2184 FLOP/B vs a ridge of
-  ~315 FLOP/B);
-* ``eager_ms`` / ``speedup_vs_eager`` — the same module run by PyTorch eager on
-  the same GPU (hipBLASLt GEMMs + elementwise kernels);
-* ``cpu_baseline`` — the CPU oracle (numpy float32, ``oracle/workloads.py``)
-  timed on this host on a bounded row sample and scaled to the full batch
-  (reported, not a target).
+* ``roofline`` — the dominant kernel's algorithmic FLOPs per launch over its
+  average launch duration (HIP events on the launch stream, inside the timed
+  region), against the 2.5 PFLOP/s bf16 dense spec and against
+  ``peak_measured``, the MFMA-only rate this device sustains at its
+  power-limited clock (``fuseml_mfma_peak_probe``, run in this process);
+  ``traffic`` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary;
+* ``configs`` — every benchmark config (C2..C5): the fused step, the same
+  module under PyTorch eager and under ``torch.compile(model,
+  backend=FuseMLCompiler())``, each the median (and quartiles) of HIP-event
+  timed iterations (at least ``--min-iters`` and ``--min-seconds``, the
+  reference's harness times >= 5 s, benchmarks/bench_mlp_block.py:544-590),
+  a cache-cold median (1 GiB written between iterations: more than the 256 MB
+  Infinity Cache), per-kernel rates, and a correctness gate: the timed fused
+  output at sampled rows against a float32 PyTorch reference (tiles rtol/atol
+  2e-2, reductions 1e-2 relative; bench_mlp_block.py:453-485), with eager
+  bf16's own error beside it as calibration;
+* ``cpu_baseline`` — the same eager module on this host's CPU cores (bf16,
+  full batch, all cores, median of timed forwards): the reference's eager
+  path, reported, not a target.
 
 One GPU only: ``--gpus`` above 1 exits with an explanation.
 """
@@ -28,6 +38,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -37,7 +48,7 @@ if REPO not in sys.path:
 
 import torch  # noqa: E402
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 spec
 HBM_PEAK_GBS = 8000.0
 
 WORKLOAD_DESC = {
@@ -47,35 +58,44 @@ WORKLOAD_DESC = {
     "C5": "Stacked MLP x4 bf16: x[8192,4096], 4 x (addmm(4096->16384)+GELU -> addmm(16384->4096)+b2+residual)",
 }
 
+RTOL = ATOL = 2e-2
+RED_RTOL = 1e-2
+
 
 def _parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="C2", choices=sorted(WORKLOAD_DESC))
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", default="C2", choices=sorted(WORKLOAD_DESC), help="headline workload")
+    p.add_argument("--configs", default="C2,C3,C4,C5",
+                   help="comma-separated configs for the per-config section ('' to skip)")
+    p.add_argument("--min-iters", type=int, default=200)
+    p.add_argument("--min-seconds", type=float, default=1.0)
+    p.add_argument("--max-seconds", type=float, default=5.0)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-eager", action="store_true", help="skip the eager GPU comparison")
+    p.add_argument("--no-compile", action="store_true", help="skip torch.compile timing")
     p.add_argument("--eager-only", action="store_true",
-                   help="run only the eager leg and print its call count (rocprof counter runs of the eager module)")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
+                   help="run only the eager leg of --workload (rocprof counter runs of the eager module)")
+    p.add_argument("--cpu-iters", type=int, default=5)
     p.add_argument("--calib-copy-mb", type=int, default=0,
                    help="after timing, run device copies of this size (rocprof counter calibration)")
     return p.parse_args()
 
 
 # ---------------------------------------------------------------------------
-# Fused pipelines: one list of (launcher, arg-builder) per workload
+# Fused pipelines: one list of (label, launcher, arg-builder, out key, gemm) per workload
 # ---------------------------------------------------------------------------
 
 
-def _build_pipeline(name: str, wl, dev):
+def _build_pipeline(name: str, wl):
     from fuseml_amd.epilogue import EpilogueSpec, EpiOp
     from fuseml_amd.launcher import HipKernelLauncher
 
     dt = wl.dtype
     m = wl.model
-    stages = []  # (label, launcher, fn(state)->args, gemm (M,N,K))
+    stages = []
 
     def mlp_block(prefix, blk, gemms):
         g1 = HipKernelLauncher(EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("gelu_erf")), dt), 3)
@@ -92,7 +112,8 @@ def _build_pipeline(name: str, wl, dev):
             mlp_block(f"B{i} ", blk, wl.gemms[2 * i: 2 * i + 2])
     elif name == "C3":
         lin = m.linear
-        spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("relu"), EpiOp("mul", 3), EpiOp("sigmoid"), EpiOp("add", 4)), dt)
+        spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("relu"), EpiOp("mul", 3), EpiOp("sigmoid"),
+                                   EpiOp("add", 4)), dt)
         g = HipKernelLauncher(spec, 5)
         stages.append(("addmm+bias+relu*g+sigmoid+row", g,
                        lambda s: (lin.bias, s["x"], lin.weight.t(), s["g"], m.row), "y", wl.gemms[0]))
@@ -122,6 +143,17 @@ def _run_pipeline(stages, state, events=None, io=None):
     return state
 
 
+def _final(name, state):
+    return state["y"] if name in ("C3", "C4") else state["x"]
+
+
+def _initial_state(name, wl):
+    st = {"x": wl.inputs[0]}
+    if name == "C3":
+        st["g"] = wl.inputs[1]
+    return st
+
+
 def _algorithmic_bytes(args, out):
     """HBM bytes a launch must move at least: every distinct input tensor read
     once (a [K,N] weight view counts its K*N elements) and every output written
@@ -135,18 +167,209 @@ def _algorithmic_bytes(args, out):
     return total
 
 
-def _initial_state(name, wl):
-    st = {"x": wl.inputs[0]}
-    if name == "C3":
-        st["g"] = wl.inputs[1]
-    return st
+# ---------------------------------------------------------------------------
+# Timing
+# ---------------------------------------------------------------------------
+
+
+def _quartiles(xs):
+    xs = sorted(xs)
+    q = statistics.quantiles(xs, n=4) if len(xs) >= 2 else [xs[0]] * 3
+    return {"median_ms": round(q[1], 4), "p25_ms": round(q[0], 4), "p75_ms": round(q[2], 4), "iters": len(xs)}
+
+
+def _time_events(fn, args, flush=None, warmup=25):
+    """HIP-event time of each fn() call on the current stream, over at least
+    args.min_iters calls and args.min_seconds (at most args.max_seconds once
+    min_iters are done).  `flush`, if given, runs untimed before each call."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    t0 = time.perf_counter()
+    while True:
+        batch = []
+        for _ in range(10):
+            if flush is not None:
+                flush()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            batch.append((s, e))
+        torch.cuda.synchronize()
+        times += [s.elapsed_time(e) for s, e in batch]
+        el = time.perf_counter() - t0
+        if len(times) >= args.min_iters and (el >= args.min_seconds or el >= args.max_seconds):
+            break
+    return _quartiles(times)
+
+
+class _Flush:
+    """Writes 1 GiB between timed iterations: more than the 256 MB Infinity
+    Cache plus the L2s, so every operand is re-read from HBM (the reference
+    flushes 128 MB, bench_mlp_block.py:436-445, sized for a 4050 Laptop's L2)."""
+
+    def __init__(self, dev):
+        self.buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        self.k = 0
+
+    def __call__(self):
+        self.k += 1
+        self.buf.fill_(float(self.k))
 
 
 # ---------------------------------------------------------------------------
-# HBM traffic per launch, from the committed rocprofv3 counter summary
+# Correctness gate: fused output at sampled rows against float32 PyTorch
+# ---------------------------------------------------------------------------
+
+
+def _sample_rows(M, n=64, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.randint(0, M, (n,), generator=g)
+    return torch.unique(torch.cat([torch.tensor([0, M - 1]), rows]))
+
+
+def _reference_rows(name, wl, rows):
+    """Float32 PyTorch forward of the workload at `rows` (rows are independent)."""
+    f = lambda t: t.float()  # noqa: E731
+    m = wl.model
+    with torch.no_grad():
+        x = f(wl.inputs[0][rows])
+        if name == "C2":
+            h = torch.nn.functional.gelu(x @ f(m.linear1.weight).t() + f(m.linear1.bias))
+            return {"tile": h @ f(m.linear2.weight).t() + f(m.linear2.bias) + x}
+        if name == "C3":
+            g = f(wl.inputs[1][rows])
+            h = torch.relu(x @ f(m.linear.weight).t() + f(m.linear.bias))
+            return {"tile": torch.sigmoid(h * g) + f(m.row)}
+        if name == "C4":
+            h = torch.relu(x @ f(m.linear.weight).t())
+            return {"tile": h, "sum": h.sum(-1), "amax": h.amax(-1), "mean": h.mean(-1)}
+        y = x
+        for blk in m.blocks:
+            h = torch.nn.functional.gelu(y @ f(blk.linear1.weight).t() + f(blk.linear1.bias))
+            y = h @ f(blk.linear2.weight).t() + f(blk.linear2.bias) + y
+        return {"tile": y}
+
+
+def _as_parts(name, out):
+    """Module-shaped output -> {"tile", and for C4 "sum", "amax", "mean"}."""
+    if name == "C4":
+        if isinstance(out, dict):
+            return out
+        h, s, mx, mean = out
+        return {"tile": h, "sum": s, "amax": mx, "mean": mean}
+    return {"tile": out}
+
+
+def _check(parts, ref, rows):
+    res = {"rows_checked": int(len(rows)), "ok": True}
+    for k, r in ref.items():
+        got = parts[k][rows].float()
+        err = (got - r).abs()
+        if k == "tile":
+            ok = bool(torch.all(err <= ATOL + RTOL * r.abs()))
+        else:
+            ok = bool(torch.all(err <= RED_RTOL * r.abs() + 1e-6))
+        res[f"{k}_max_abs_err"] = float(err.max())
+        res["ok"] = res["ok"] and ok
+    return res
+
+
+# ---------------------------------------------------------------------------
+# Per-config section
+# ---------------------------------------------------------------------------
+
+
+def _c4_fused_parts(state):
+    s, mx, mean, h = state["y"]
+    return {"tile": h, "sum": s, "amax": mx, "mean": mean}
+
+
+def _config_detail(name, args, dev, peak_tflops, flush):
+    from fuseml_amd.compiler import FuseMLCompiler
+    from fuseml_amd.workloads import WORKLOADS
+
+    wl = WORKLOADS[name]()
+    wl.to(dev)
+    rows = _sample_rows(wl.inputs[0].shape[0]).to(dev)
+    ref = _reference_rows(name, wl, rows)
+    stages = _build_pipeline(name, wl)
+    st0 = _initial_state(name, wl)
+    last = {}
+
+    def fused():
+        last["state"] = _run_pipeline(stages, dict(st0))
+
+    out = {"workload": WORKLOAD_DESC[name], "gemms_MNK": wl.gemms, "gflop": round(wl.flops / 1e9, 1)}
+    with torch.no_grad():
+        out["fused"] = _time_events(fused, args)
+        state = last["state"]
+        parts = _c4_fused_parts(state) if name == "C4" else {"tile": _final(name, state)}
+        out["fused"]["check"] = _check(parts, ref, rows)
+        out["fused"]["tflops"] = round(wl.flops / (out["fused"]["median_ms"] * 1e-3) / 1e12, 1)
+        out["fused_cold"] = _time_events(fused, args, flush=flush)
+
+        # per-kernel event times (the same launches, 50 steps)
+        n = 50
+        ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in stages]
+              for _ in range(n)]
+        for k in range(n):
+            _run_pipeline(stages, dict(st0), ev[k])
+        torch.cuda.synchronize()
+        kernels = []
+        for i, (label, _, _, _, (Mg, Ng, Kg)) in enumerate(stages):
+            avg = sum(ev[k][i][0].elapsed_time(ev[k][i][1]) for k in range(n)) / n
+            tf = 2.0 * Mg * Ng * Kg / (avg * 1e-3) / 1e12
+            kernels.append({"kernel": label, "avg_ms": round(avg, 4), "tflops": round(tf, 1),
+                            "frac_spec": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                            "frac_measured_peak": round(tf / peak_tflops, 4) if peak_tflops else None})
+        if name == "C5":  # blocks repeat the same two shapes: report one of each
+            kernels = kernels[:2]
+        out["kernels"] = kernels
+        dom = max(kernels, key=lambda k: k["avg_ms"])
+        out["dominant_frac_spec"] = dom["frac_spec"]
+
+        if not args.no_eager:
+            out["eager"] = _time_events(lambda: wl.model(*wl.inputs), args)
+            eo = wl.model(*wl.inputs)
+            out["eager"]["check"] = _check(_as_parts(name, eo), ref, rows)
+            out["speedup_vs_eager"] = round(out["eager"]["median_ms"] / out["fused"]["median_ms"], 3)
+        if not args.no_compile:
+            torch._dynamo.reset()
+            be = FuseMLCompiler(fuse_sibling_reductions=(name == "C4"))
+            compiled = torch.compile(wl.model, backend=be)
+            t0 = time.perf_counter()
+            co = compiled(*wl.inputs)
+            torch.cuda.synchronize()
+            comp = {"first_call_s": round(time.perf_counter() - t0, 2),
+                    "fusion_strategy": be.fusion_strategy,
+                    "hip_launchers": len({id(x) for x in be.launchers})}
+            comp.update(_time_events(lambda: compiled(*wl.inputs), args))
+            comp["check"] = _check(_as_parts(name, co), ref, rows)
+            out["compiled"] = comp
+    del wl, stages, st0, last
+    torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic per launch, from the committed rocprofv3 counter summaries
 # ---------------------------------------------------------------------------
 
 TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "traffic_{workload}.md")
+EAGER_TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "traffic_eager_{workload}.md")
+MFMA_BUSY_SUMMARY = os.path.join(REPO, "profiles", "mfma_busy_{workload}.md")
+
+
+def _json_block(path):
+    if not os.path.exists(path):
+        return None
+    text = open(path).read()
+    if "```json" not in text:
+        return None
+    return json.loads(text.split("```json", 1)[1].split("```", 1)[0])
 
 
 def _traffic(workload, launch):
@@ -163,16 +386,16 @@ def _traffic(workload, launch):
     return None
 
 
-EAGER_TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "traffic_eager_{workload}.md")
-
-
-def _json_block(path):
-    if not os.path.exists(path):
+def _mfma_busy(workload, launch):
+    """MFMA-busy fraction of the launch from the committed counter summary
+    (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x CUs), or None."""
+    data = _json_block(MFMA_BUSY_SUMMARY.format(workload=workload))
+    if data is None:
         return None
-    text = open(path).read()
-    if "```json" not in text:
-        return None
-    return json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    for k in data.get("kernels", []):
+        if k.get("launch") == launch:
+            return k.get("mfma_busy_frac")
+    return None
 
 
 def _hbm_traffic(workload, gemms):
@@ -215,56 +438,83 @@ def _hbm_traffic(workload, gemms):
 
 
 # ---------------------------------------------------------------------------
-# CPU oracle baseline (bounded sample, scaled to the full batch)
+# Measured MFMA peak and the CPU baseline
 # ---------------------------------------------------------------------------
 
 
-def _cpu_baseline(name, wl, seconds):
-    import numpy as np
-    from threadpoolctl import threadpool_info, threadpool_limits
+def _mfma_peak(dev, seconds=0.3):
+    """bf16 MFMA TFLOP/s that this device sustains: fuseml_mfma_peak_probe (MFMAs
+    only, random register operands, every SIMD of every CU) timed with HIP
+    events; the median of 5 launches of about `seconds` each."""
+    import ctypes
 
-    from oracle import workloads as ora_w
+    from fuseml_amd import _abi
+
+    lib = _abi.load_library()
+    wgs = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    flop_per_iter = wgs * 4 * 8 * 2 * 32 * 32 * 16
+
+    def run(iters):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        rc = lib.fuseml_mfma_peak_probe(ctypes.c_int64(iters), wgs, ctypes.c_void_p(sink.data_ptr()),
+                                        ctypes.c_void_p(stream.cuda_stream))
+        e.record()
+        if rc != 0:
+            raise RuntimeError(f"fuseml_mfma_peak_probe: {rc}")
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e-3
+
+    dt = run(2000)
+    iters = max(2000, int(2000 * seconds / max(dt, 1e-6)))
+    rates = sorted(flop_per_iter * iters / run(iters) / 1e12 for _ in range(5))
+    return {"tflops": round(rates[2], 1), "kernel": "fuseml_mfma_peak_probe (v_mfma_f32_32x32x16_bf16 only)",
+            "iters": iters, "workgroups": wgs}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_baseline(name, iters):
+    """The workload's eager nn.Module on this host's CPU: bf16 (fp32 for C1),
+    full batch, torch.set_num_threads(len(sched_getaffinity)), one warm-up
+    forward then the median of `iters` timed forwards (perf_counter)."""
+    from fuseml_amd.workloads import WORKLOADS
 
     cores = len(os.sched_getaffinity(0))
-    f32 = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
-    m = wl.model
-    x = f32(wl.inputs[0])
-    M = x.shape[0]
-    rows = np.arange(min(M, 256))
-    if name in ("C2",):
-        args = (f32(m.linear1.weight), f32(m.linear1.bias), f32(m.linear2.weight), f32(m.linear2.bias))
-        fn = lambda: ora_w.transformer_mlp(x, *args, rows=rows, dtype=np.float32)  # noqa: E731
-    elif name == "C3":
-        g = f32(wl.inputs[1])
-        args = (f32(m.linear.weight), f32(m.linear.bias), g, f32(m.row))
-        fn = lambda: ora_w.activation_heavy(x, *args, rows=rows, dtype=np.float32)  # noqa: E731
-    elif name == "C4":
-        w = f32(m.linear.weight)
-        fn = lambda: ora_w.gemm_row_reductions(x, w, rows=rows, dtype=np.float32)  # noqa: E731
-    else:
-        blocks = [(f32(b.linear1.weight), f32(b.linear1.bias), f32(b.linear2.weight), f32(b.linear2.bias))
-                  for b in m.blocks]
-        rows = np.arange(min(M, 64))
-        fn = lambda: ora_w.stacked_mlp(x, blocks, rows=rows, dtype=np.float32)  # noqa: E731
-    with threadpool_limits(limits=cores):
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-        fn()  # warm-up
-        t0 = time.perf_counter()
-        reps = 0
-        while True:
-            fn()
-            reps += 1
-            if time.perf_counter() - t0 >= seconds:
-                break
-        dt = (time.perf_counter() - t0) / reps
-    ms_full = dt * 1e3 * (M / len(rows))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        wl = WORKLOADS[name]()  # CPU tensors, same seeds as the GPU run
+        with torch.no_grad():
+            wl.model(*wl.inputs)
+            ts = []
+            for _ in range(iters):
+                t0 = time.perf_counter()
+                wl.model(*wl.inputs)
+                ts.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
+    ms = statistics.median(ts) * 1e3
     return {
-        "value": round(ms_full, 3),
-        "unit": "ms per full-batch forward (extrapolated from a row sample)",
-        "cores": int(threads),
-        "kind": "port",
-        "sample": f"oracle/workloads.py numpy float32 forward of {len(rows)} of {M} rows, "
-                  f"{reps} repetitions in {dt * reps:.1f} s, scaled by {M / len(rows):.0f}",
+        "value": round(ms, 2),
+        "unit": "ms per full-batch forward",
+        "cores": cores,
+        "kind": "reference",
+        "sample": f"{name} eager PyTorch module (the reference's bypass path, gm.forward) on the CPU, "
+                  f"{str(wl.dtype).replace('torch.', '')}, full batch, torch.set_num_threads({cores}), "
+                  f"1 warm-up + median of {iters} forwards ({sum(ts):.1f} s)",
+        "cpu_model": _cpu_model(),
+        "gflops": round(wl.flops / (ms * 1e-3) / 1e9, 1),
     }
 
 
@@ -313,30 +563,31 @@ def main():
 
     name = args.workload
     dev = torch.device("cuda:0")
-    wl = WORKLOADS[name]()
-    wl.to(dev)
     torch.backends.cuda.matmul.allow_tf32 = False
 
     if args.eager_only:
+        wl = WORKLOADS[name]()
+        wl.to(dev)
         _calib_copy(args.calib_copy_mb, dev)
         calls, eager_ms = _run_eager(wl, args.warmup, args.steps)
         print(json.dumps({"workload": name, "eager_ms": round(eager_ms, 4), "eager_calls": calls}), flush=True)
         return
 
-    stages = _build_pipeline(name, wl, dev)
+    # ---- headline: exactly K timed steps of the fused pipeline ----
+    wl = WORKLOADS[name]()
+    wl.to(dev)
+    stages = _build_pipeline(name, wl)
     with torch.no_grad():
         state = _initial_state(name, wl)
         for _ in range(args.warmup):
             _run_pipeline(stages, dict(state))
         torch.cuda.synchronize()
-
         events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for _ in stages] for _ in range(args.steps)]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for k in range(args.steps):
-            ev = [events[k][i] for i in range(len(stages))]
-            _run_pipeline(stages, dict(state), ev)
+            _run_pipeline(stages, dict(state), events[k])
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
@@ -346,10 +597,8 @@ def main():
         durs = [events[k][i][0].elapsed_time(events[k][i][1]) for k in range(args.steps)]
         avg = sum(durs) / len(durs)
         Mg, Ng, Kg = gemm
-        flops = 2.0 * Mg * Ng * Kg
         per_kernel.append({"kernel": label, "avg_ms": round(avg, 4), "gemm_MNK": [Mg, Ng, Kg],
-                           "tflops": round(flops / (avg * 1e-3) / 1e12, 1)})
-    # one more (untimed) pass to read each launch's operands and outputs
+                           "tflops": round(2.0 * Mg * Ng * Kg / (avg * 1e-3) / 1e12, 1)})
     io = []
     with torch.no_grad():
         _run_pipeline(stages, dict(state), io=io)
@@ -361,16 +610,29 @@ def main():
     dk = per_kernel[dom]
     Mg, Ng, Kg = dk["gemm_MNK"]
     achieved = 2.0 * Mg * Ng * Kg / (dk["avg_ms"] * 1e-3) / 1e12
-
+    del io
     _calib_copy(args.calib_copy_mb, dev)
 
-    eager_ms = None
+    peak = _mfma_peak(dev)
+    headline_eager = None
     if not args.no_eager:
-        _, eager_ms = _run_eager(wl, args.warmup, args.steps)
+        _, headline_eager = _run_eager(wl, args.warmup, args.steps)
+    del wl, stages, state
+    torch.cuda.empty_cache()
+
+    # ---- per-config section ----
+    configs = {}
+    flush = _Flush(dev) if args.configs else None
+    for c in [c for c in args.configs.split(",") if c]:
+        print(f"[bench] config {c}", file=sys.stderr, flush=True)
+        configs[c] = _config_detail(c, args, dev, peak["tflops"], flush)
+    del flush
+    torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
-        cpu = _cpu_baseline(name, wl, args.cpu_seconds)
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        cpu = _cpu_baseline(name, args.cpu_iters)
 
     line = {
         "metric": "fused MLP-block latency (ms), % HBM/MFMA roofline, speedup vs eager",
@@ -385,11 +647,10 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded torch.Generator inputs, random-init nn.Linear weights)",
-        "config": {"workload": f"{name}: {WORKLOAD_DESC[name]}", "gemms_MNK": wl.gemms,
+        "config": {"workload": f"{name}: {WORKLOAD_DESC[name]}", "gemms_MNK": _gemms_of(name),
                    "parallelism": "single GPU"},
-        "tflops_per_step": round(wl.flops / (ms_per_step * 1e-3) / 1e12, 1),
-        "eager_ms": None if eager_ms is None else round(eager_ms, 4),
-        "speedup_vs_eager": None if eager_ms is None else round(eager_ms / ms_per_step, 3),
+        "eager_ms": None if headline_eager is None else round(headline_eager, 4),
+        "speedup_vs_eager": None if headline_eager is None else round(headline_eager / ms_per_step, 3),
         "kernels": per_kernel,
         "roofline": {
             "bound": "mfma",
@@ -399,16 +660,31 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": _traffic(name, dom),
+            "peak_measured": peak["tflops"],
+            "frac_of_measured": round(achieved / peak["tflops"], 4),
+            "peak_probe": peak,
+            "mfma_busy_frac": _mfma_busy(name, dom),
         },
         # the same dominant kernel against the HBM roofline: algorithmic bytes
         # (inputs and outputs once) over its event-timed duration
         "hbm_roofline": {"kernel": dk["kernel"], "algorithmic_bytes": dk["algorithmic_bytes"],
                          "achieved": dk["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(dk["GBps"] / HBM_PEAK_GBS, 4)},
-        "hbm_traffic": _hbm_traffic(name, wl.gemms),
+        "hbm_traffic": _hbm_traffic(name, [tuple(g) for g in _gemms_of(name)]),
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def _gemms_of(name):
+    """(M, N, K) of each GEMM of one forward of `name` (no tensors built)."""
+    return {
+        "C2": [[16384, 4096, 1024], [16384, 1024, 4096]],
+        "C3": [[16384, 4096, 1024]],
+        "C4": [[8192, 8192, 2048]],
+        "C5": [[8192, 16384, 4096], [8192, 4096, 16384]] * 4,
+    }[name]
 
 
 if __name__ == "__main__":

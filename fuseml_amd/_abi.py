@@ -67,10 +67,12 @@ EXPORTED_SYMBOLS = (
     "fuseml_gemm_epilogue",
     "fuseml_gemm_epilogue_supported",
     "fuseml_gemm_epilogue_config",
+    "fuseml_gemm_epilogue_force_variant",
     "fuseml_last_error",
     "fuseml_device_arch",
     "fuseml_abi_version",
     "fuseml_desc_size",
+    "fuseml_mfma_peak_probe",
 )
 
 
@@ -150,12 +152,16 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fuseml_gemm_epilogue_supported.restype = ctypes.c_int
     lib.fuseml_gemm_epilogue_config.argtypes = [desc_p, ctypes.POINTER(ctypes.c_int32)]
     lib.fuseml_gemm_epilogue_config.restype = ctypes.c_int
+    lib.fuseml_gemm_epilogue_force_variant.argtypes = [ctypes.c_char_p]
+    lib.fuseml_gemm_epilogue_force_variant.restype = ctypes.c_int
     lib.fuseml_last_error.argtypes = []
     lib.fuseml_last_error.restype = ctypes.c_char_p
     lib.fuseml_device_arch.argtypes = [ctypes.c_int, ctypes.c_char_p, ctypes.c_int]
     lib.fuseml_device_arch.restype = ctypes.c_int
     lib.fuseml_abi_version.argtypes = []
     lib.fuseml_abi_version.restype = ctypes.c_int
+    lib.fuseml_mfma_peak_probe.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.fuseml_mfma_peak_probe.restype = ctypes.c_int
     lib.fuseml_desc_size.argtypes = []
     lib.fuseml_desc_size.restype = ctypes.c_size_t
 
@@ -188,6 +194,20 @@ def load_library() -> ctypes.CDLL:
         check_abi(lib)
         _lib = lib
         return lib
+
+
+VARIANTS = ("large", "deep", "deep3", "small")
+
+
+def force_variant(name: Optional[str]) -> None:
+    """Pin the kernel variant for later launches in this process (None: automatic).
+
+    ``FUSEML_HIP_TILE`` gives the initial value and is read once per process;
+    this is how tests and tuning sweeps change it afterwards."""
+    lib = load_library()
+    rc = lib.fuseml_gemm_epilogue_force_variant(None if name is None else name.encode())
+    if rc != OK:
+        raise ValueError(last_error(lib))
 
 
 def last_error(lib: ctypes.CDLL) -> str:

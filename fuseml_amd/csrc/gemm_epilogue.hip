@@ -102,6 +102,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
   return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), kRsrcWord3);
 }
 
+// Buffer resource over [p + skip, p + total): the caller's offsets are relative
+// to p + skip, so only the span one tile touches must fit the 32-bit offsets
+// (the host checks that), not the whole operand.  The record count is clamped
+// to 2^31 - 1; an offset at or past it reads zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_at(const void* p, int64_t skip, int64_t total) {
+  const int64_t rest = total - skip;
+  const uint32_t bytes = rest <= 0 ? 0u : (rest >= 0x7fffffffLL ? 0x7fffffffu : (uint32_t)rest);
+  return make_rsrc(static_cast<const char*>(p) + skip, bytes);
+}
+
 template <typename T>
 __device__ __forceinline__ f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c);
 
@@ -137,7 +147,8 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
   // Saturate to the finite fp16 range before narrowing
   // (fuseml/codegen/kernel_generator.py:1575-1581).
-  x = fminf(fmaxf(x, -kFp16Max), kFp16Max);
+  // NaN is kept (the clamp alone would turn it into -65504).
+  x = __builtin_isnan(x) ? x : fminf(fmaxf(x, -kFp16Max), kFp16Max);
   _Float16 h = (_Float16)x;
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
@@ -153,21 +164,23 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 }
 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
-  a = fminf(fmaxf(a, -kFp16Max), kFp16Max);
-  b = fminf(fmaxf(b, -kFp16Max), kFp16Max);
+  a = __builtin_isnan(a) ? a : fminf(fmaxf(a, -kFp16Max), kFp16Max);
+  b = __builtin_isnan(b) ? b : fminf(fmaxf(b, -kFp16Max), kFp16Max);
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
 }
 
 __device__ __forceinline__ int dtype_bytes(int dtype) { return dtype == FUSEML_F32 ? 4 : 2; }
 
-// Load the 4 operand values at (m, n..n+3).  `ok` says the whole run of four is
-// inside [0,M) x [0,N); an invalid run reads zeros through the buffer bound.
+// Load the 4 operand values at (m, n..n+3) of the tile at (m0, n0).  `ok` says
+// the whole run of four is inside [0,M) x [0,N); an invalid run reads zeros
+// through the buffer bound.  Offsets are relative to the tile origin.
 template <typename Op>
-__device__ __forceinline__ void load_operand4(const Op& op, int m, int n, bool ok, float v[4]) {
+__device__ __forceinline__ void load_operand4(const Op& op, int m0, int n0, int m, int n, bool ok, float v[4]) {
   const int dt = op.dtype;
   const int eb = dtype_bytes(dt);
-  const __amdgpu_buffer_rsrc_t r = make_rsrc(op.ptr, (uint32_t)(op.extent * eb));
-  const int64_t base = (int64_t)m * op.stride_m + (int64_t)n * op.stride_n;
+  const __amdgpu_buffer_rsrc_t r =
+      make_rsrc_at(op.ptr, ((int64_t)m0 * op.stride_m + (int64_t)n0 * op.stride_n) * eb, op.extent * eb);
+  const int64_t base = (int64_t)(m - m0) * op.stride_m + (int64_t)(n - n0) * op.stride_n;
   if (op.reserved & kFlagVec4) {
     // Unit stride along N and 4-element aligned rows: one vector load.
     const uint32_t off = ok ? (uint32_t)(base * eb) : kOOB;
@@ -230,12 +243,23 @@ __device__ __forceinline__ void store_out4(const Out& o, int m, int n, int M, in
 }
 
 // Float atomic max through integer atomics: non-negative floats order like
-// signed ints, negative floats order inversely like unsigned ints.
+// signed ints, negative floats order inversely like unsigned ints.  A NaN is
+// written as the positive quiet NaN 0x7fc00000, which as a signed int exceeds
+// every positive float (so later signed maxima keep it) and as an unsigned int
+// is below every negative float (so later unsigned minima keep it): the
+// result is NaN once any partial is, as in torch.amax.
 __device__ __forceinline__ void atomic_max_f32(float* p, float v) {
-  if (v >= 0.0f)
+  if (__builtin_isnan(v))
+    atomicMax(reinterpret_cast<int*>(p), 0x7fc00000);
+  else if (v >= 0.0f)
     atomicMax(reinterpret_cast<int*>(p), __float_as_int(v));
   else
     atomicMin(reinterpret_cast<unsigned int*>(p), __float_as_uint(v));
+}
+
+// max(a, b), NaN if either is NaN (fmaxf returns the other operand).
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return __builtin_isunordered(a, b) ? __builtin_nanf("") : fmaxf(a, b);
 }
 
 // Standard normal CDF for GELU (approximate='none'):
@@ -487,11 +511,12 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     const int m0 = pid_m * BM;
     const int n0 = pid_n * BN;
 
-    // Operand buffer resources (the host guarantees the byte extents fit in 31 bits).
-    const uint32_t a_bytes = (uint32_t)(((int64_t)(M - 1) * d.lda + K) * 2);
-    const uint32_t b_bytes = (uint32_t)(((int64_t)(N - 1) * d.ldb + K) * 2);
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(d.a, a_bytes);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(d.b, b_bytes);
+    // Operand buffer resources based at the tile's first row of A and of W, so
+    // that only a tile's rows need 32-bit offsets (the host checks that span).
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc_at(d.a, (int64_t)m0 * d.lda * 2, ((int64_t)(M - 1) * d.lda + K) * 2);
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc_at(d.b, (int64_t)n0 * d.ldb * 2, ((int64_t)(N - 1) * d.ldb + K) * 2);
 
     // Vector operands with an LDS slot (bias and the like): this thread's element
     // of each is loaded now, lands during the K loop, and is written to its slot
@@ -507,8 +532,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       const bool ok = tid < (rowv ? BN : BM) && idx < (rowv ? N : M);
       const int64_t st = rowv ? d.operands[oi].stride_n : d.operands[oi].stride_m;
       const int eb = d.operands[oi].dtype == FUSEML_F32 ? 4 : 2;
-      const __amdgpu_buffer_rsrc_t r = make_rsrc(d.operands[oi].ptr, (uint32_t)(d.operands[oi].extent * eb));
-      const uint32_t off = ok ? (uint32_t)((int64_t)idx * st * eb) : kOOB;
+      const __amdgpu_buffer_rsrc_t r = make_rsrc_at(d.operands[oi].ptr, (int64_t)(rowv ? n0 : m0) * st * eb,
+                                                    d.operands[oi].extent * eb);
+      const uint32_t off = ok ? (uint32_t)((int64_t)tid * st * eb) : kOOB;
       const uint32_t bits = (eb == 4) ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)
                                       : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
       const int slot = (fl >> 8) & (kAuxSlots - 1);
@@ -548,21 +574,22 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
                   "operand DMAs line up with the stage DMAs");
     const bool op_dma = kOpDma && staged >= 0;
     const void* op_ptr = d.a;
-    uint32_t op_bytes = a_bytes;
+    int64_t op_bytes = 0;  // bytes of the operand from its row m0 on
     uint32_t op_o[kOpDma ? LPS : 1];  // chunk c's byte offset in its slot (kOOB: column past N)
     uint64_t op_row_bytes = 0;        // operand row pitch in bytes
     uint32_t op_osm = 0;
     if constexpr (kOpDma) {
       const int si = staged >= 0 ? staged : 0;
-      op_ptr = d.operands[si].ptr;
-      op_bytes = (uint32_t)(d.operands[si].extent * 2);
       const uint32_t osm = (uint32_t)d.operands[si].stride_m;
       op_osm = osm;
       op_row_bytes = (uint64_t)osm * 2u;
+      // Based at the tile's first row: offsets cover the tile's rows only.
+      op_ptr = static_cast<const char*>(d.operands[si].ptr) + (uint64_t)m0 * op_row_bytes;
+      op_bytes = d.operands[si].extent * 2 - (int64_t)m0 * (int64_t)op_row_bytes;
       if constexpr (SCHED != 6) static_for<0, LPS>([&](auto c) {
         const int r = (wave + NW * c) * RPD + lane / CPR;
         const int n = n0 + 8 * ((lane % CPR) ^ (r & 31));
-        op_o[c] = n < N ? ((uint32_t)(m0 + r) * osm + (uint32_t)n) * 2u : kOOB;
+        op_o[c] = n < N ? ((uint32_t)r * osm + (uint32_t)n) * 2u : kOOB;
       });
     }
     // Base and byte extent of slot `slot`'s part of the operand.
@@ -570,8 +597,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       return static_cast<const char*>(op_ptr) + (uint64_t)(slot * RPS) * op_row_bytes;
     };
     auto op_slot_bytes = [&](int slot) -> uint32_t {
-      const uint64_t skip = (uint64_t)(slot * RPS) * op_row_bytes;
-      return skip < op_bytes ? op_bytes - (uint32_t)skip : 0u;
+      const int64_t rest = op_bytes - (int64_t)(slot * RPS) * (int64_t)op_row_bytes;
+      return rest <= 0 ? 0u : (rest >= 0x7fffffffLL ? 0x7fffffffu : (uint32_t)rest);
     };
     // Operand chunks [c0, c1) of slot `slot`.
     auto load_op_chunks = [&](int slot, auto c0, auto c1) {
@@ -582,7 +609,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         if constexpr (SCHED == 6) {  // computed here: 16 fewer registers held across the K loop
           const int r = (wave + NW * c) * RPD + lane / CPR;
           const int n = n0 + 8 * ((lane % CPR) ^ (r & 31));
-          oo = n < N ? ((uint32_t)(m0 + r) * op_osm + (uint32_t)n) * 2u : kOOB;
+          oo = n < N ? ((uint32_t)r * op_osm + (uint32_t)n) * 2u : kOOB;
         } else {
           oo = op_o[c];
         }
@@ -602,14 +629,14 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     static_for<0, A_DMA>([&](auto i) {
       const int row = (wave + NW * i) * G::kRowsPerDma + lane / G::kChunks;
       const int kc = (lane % G::kChunks) ^ G::swizzle(row);
-      const int gm = min(m0 + row, M - 1);
+      const int gm = min(row, M - 1 - m0);
       a_off[i] = (uint32_t)((int64_t)gm * d.lda * 2) + (uint32_t)(kc * 16);
       a_k[i] = kc * 8;
     });
     static_for<0, B_DMA>([&](auto i) {
       const int row = (wave + NW * i) * G::kRowsPerDma + lane / G::kChunks;
       const int kc = (lane % G::kChunks) ^ G::swizzle(row);
-      const int gn = min(n0 + row, N - 1);
+      const int gn = min(row, N - 1 - n0);
       b_off[i] = (uint32_t)((int64_t)gn * d.ldb * 2) + (uint32_t)(kc * 16);
       b_k[i] = kc * 8;
     });
@@ -1092,7 +1119,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     if (staged >= 0 && !op_dma) {
       const void* optr = d.operands[staged].ptr;
       const int64_t osm = d.operands[staged].stride_m;
-      const __amdgpu_buffer_rsrc_t r = make_rsrc(optr, (uint32_t)(d.operands[staged].extent * 2));
+      const __amdgpu_buffer_rsrc_t r = make_rsrc_at(optr, (int64_t)m0 * osm * 2, d.operands[staged].extent * 2);
       // Batches of 8 passes: the loads of a batch are all in flight before the
       // first LDS write.  Offsets in 32-bit arithmetic (exact for every in-range
       // element: the host bounds the operand's span below 2 GiB) and selected,
@@ -1105,7 +1132,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         static_for<0, PB>([&](auto q) {
           const int rl = (b * PB + q) * RPP + crow;
           const int m = m0 + rl, n = n0 + 8 * cchk;
-          const uint32_t o32 = ((uint32_t)m * (uint32_t)osm + (uint32_t)n) * 2u;
+          const uint32_t o32 = ((uint32_t)rl * (uint32_t)osm + (uint32_t)n) * 2u;
           x[q] = __builtin_amdgcn_raw_buffer_load_b128(r, (m < M && n < N) ? o32 : kOOB, 0, 0);
         });
         static_for<0, PB>([&](auto q) {
@@ -1127,10 +1154,15 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // chains).  16 instead of 8 for the one-wave schedule measured no faster.
     constexpr int EW = 8;
     const bool out_bf16 = d.out.dtype == FUSEML_BF16;
-    float rs[NJ], rmx[NJ];  // row partials (sum, max) of this lane's rows
+    // Row partials (sum, max) of this lane's rows.  The max partial uses fmaxf
+    // (one VALU op per element) and a NaN seen in the row is recorded in rnan,
+    // applied when the partials are combined.
+    float rs[NJ], rmx[NJ];
+    bool rnan[NJ];
     static_for<0, NJ>([&](auto j) {
       rs[j] = 0.0f;
       rmx[j] = -INFINITY;
+      rnan[j] = false;
     });
     float* red_sum = reinterpret_cast<float*>(smem);
     float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
@@ -1202,7 +1234,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
               float x[16];
               static_for<0, 4>([&](auto g) {
                 const int n = nb + 8 * g;
-                load_operand4(d.operands[oi], m, n, m < M && n < N, x + 4 * g);
+                load_operand4(d.operands[oi], m0, n0, m, n, m < M && n < N, x + 4 * g);
               });
               combine(A[j], x);
             });
@@ -1226,8 +1258,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       A[j][(int)r] = (expr);                        \
     });                                                  \
   })
-          case FUSEML_OP_RELU:
-            FUSEML_EACH(v > 0.0f ? v : 0.0f);
+          case FUSEML_OP_RELU:  // NaN passes through, as in torch.relu
+            FUSEML_EACH(v < 0.0f ? 0.0f : v);
             break;
 #define FUSEML_EACH_N(fn)                                \
   static_for<0, NJ>([&](auto j) {                        \
@@ -1272,9 +1304,11 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       // output overwrites the staged operand in place: each 8-byte unit is read
       // (above) and written (here) by the same lane.
       float cs[16], cmx[16];
+      bool cnan[16];
       static_for<0, 16>([&](auto r) {
         cs[r] = 0.0f;
         cmx[r] = -INFINITY;
+        cnan[r] = false;
       });
       static_for<0, NJ>([&](auto j) {
         const int m = mw + 32 * j;
@@ -1320,10 +1354,12 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
             if (row_red && in) {
               rs[j] += x;
               rmx[j] = fmaxf(rmx[j], x);
+              rnan[j] |= __builtin_isnan(x);
             }
             if (col_red && in) {
               cs[r] += x;
               cmx[r] = fmaxf(cmx[r], x);
+              cnan[r] |= __builtin_isnan(x);
             }
           });
         }
@@ -1333,10 +1369,11 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         // reductions use neither a staged output nor a staged operand (the host
         // does not flag them), so the staging tile's LDS is free here.
         static_for<0, 16>([&](auto r) {
+          if (cnan[r]) cmx[r] = __builtin_nanf("");
   #pragma unroll
           for (int sh = 1; sh < 32; sh <<= 1) {
             cs[r] += __shfl_xor(cs[r], sh);
-            cmx[r] = fmaxf(cmx[r], __shfl_xor(cmx[r], sh));
+            cmx[r] = nan_max(cmx[r], __shfl_xor(cmx[r], sh));
           }
           if (l32 == 0) {
             const int col = wn * TN + 32 * i + 8 * (r >> 2) + 4 * khalf + (r & 3);
@@ -1412,8 +1449,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       if (use_stage_out || staged >= 0) __syncthreads();
       // Row partials: the other half-wave holds the other 4-column runs of the same rows.
       static_for<0, NJ>([&](auto j) {
+        const float m1 = rnan[j] ? __builtin_nanf("") : rmx[j];
         const float s2 = rs[j] + __shfl_xor(rs[j], 32);
-        const float m2 = fmaxf(rmx[j], __shfl_xor(rmx[j], 32));
+        const float m2 = nan_max(m1, __shfl_xor(m1, 32));
         if (lane < 32) {
           const int row = wm * TM + 32 * j + lane;
           red_sum[wn * BM + row] = s2;
@@ -1434,7 +1472,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       float s = 0.0f, mx = -INFINITY;
       for (int w = 0; w < nparts; ++w) {
         s += red_sum[w * len + t];
-        mx = fmaxf(mx, red_max[w * len + t]);
+        mx = nan_max(mx, red_max[w * len + t]);
       }
       if (d.reduce_mask & FUSEML_RED_SUM) atomicAdd(d.reduce_out[0] + idx, s);
       if (d.reduce_mask & FUSEML_RED_AMAX) atomic_max_f32(d.reduce_out[1] + idx, mx);
@@ -1470,18 +1508,44 @@ constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2, 0};  // 4 waves lock-step,
 constexpr TileConfig kDeep3 = {256, 256, 64, 2, 2, 2, 6};  // as kDeep, whole-stage fragments; K % 64 == 0
 
 constexpr int64_t kMaxBytes = (int64_t)1 << 31;
+constexpr int64_t kTileSpan = 256;  // largest tile edge of any variant
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Pinned variant: 0 automatic, else 1 + index into {large, deep, deep3, small}.
+// Initialised once per process from FUSEML_HIP_TILE, changed only through
+// fuseml_gemm_epilogue_force_variant.
+constexpr const char* kVariantNames[] = {"large", "deep", "deep3", "small"};
+std::atomic<int> g_forced_variant{-1};  // -1: environment not read yet
+
+int variant_code(const char* name) {
+  if (name == nullptr || name[0] == '\0' || !strcmp(name, "auto")) return 0;
+  for (int i = 0; i < 4; ++i)
+    if (!strcmp(name, kVariantNames[i])) return i + 1;
+  return -1;
+}
+
+int forced_variant() {
+  int v = g_forced_variant.load(std::memory_order_relaxed);
+  if (v < 0) {
+    const int e = variant_code(getenv("FUSEML_HIP_TILE"));
+    int expected = -1;
+    g_forced_variant.compare_exchange_strong(expected, e < 0 ? 0 : e, std::memory_order_relaxed);
+    v = g_forced_variant.load(std::memory_order_relaxed);
+  }
+  return v;
+}
+
 // `cus`: the device's CU count (the 256-wide variants run one workgroup per CU).
 TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
-  // FUSEML_HIP_TILE=large|deep|deep3|small pins a variant (tuning sweeps;
-  // deep3 falls back to deep when K % 64 != 0).
-  if (const char* force = getenv("FUSEML_HIP_TILE")) {
-    if (!strcmp(force, "large")) return kLarge;
-    if (!strcmp(force, "deep")) return kDeep;
-    if (!strcmp(force, "small")) return kSmall;
-    if (!strcmp(force, "deep3")) return d.K % 64 == 0 ? kDeep3 : kDeep;
+  // A pinned variant (tuning sweeps and the per-variant parity tests; deep3
+  // falls back to deep when K % 64 != 0).
+  switch (forced_variant()) {
+    case 1: return kLarge;
+    case 2: return kDeep;
+    case 3: return d.K % 64 == 0 ? kDeep3 : kDeep;
+    case 4: return kSmall;
+    default: break;
   }
   // A 256x256 tile keeps the LDS traffic per MFMA low enough for the MFMA pipe
   // to stay busy; below one full wave of 256-tile work the 128x128 variant
@@ -1545,9 +1609,12 @@ int validate(const fuseml_gemm_desc* dp) {
     set_error("row stride smaller than K");
     return FUSEML_EINVAL;
   }
-  if (d.K > 0 &&
-      (((d.M - 1) * d.lda + d.K) * 2 >= kMaxBytes || ((d.N - 1) * d.ldb + d.K) * 2 >= kMaxBytes)) {
-    set_error("GEMM operand spans 2 GiB or more");
+  // Buffer resources are based at each tile's origin: the rows one tile reads
+  // must span less than 2 GiB (the whole operand may be larger).
+  const int64_t tm = d.M < kTileSpan ? d.M : kTileSpan, tn = d.N < kTileSpan ? d.N : kTileSpan;
+  if (d.K > 0 && (((tm - 1) * d.lda + d.K) * 2 >= kMaxBytes || ((tn - 1) * d.ldb + d.K) * 2 >= kMaxBytes)) {
+    set_error("GEMM operand rows of one tile span 2 GiB or more (lda=%lld ldb=%lld)", (long long)d.lda,
+              (long long)d.ldb);
     return FUSEML_EUNSUPPORTED;
   }
   if (d.n_ops < 0 || d.n_ops > FUSEML_MAX_OPS || d.n_operands < 0 ||
@@ -1568,8 +1635,8 @@ int validate(const fuseml_gemm_desc* dp) {
                 (long long)need);
       return FUSEML_EINVAL;
     }
-    if (op.extent * (op.dtype == FUSEML_F32 ? 4 : 2) >= kMaxBytes) {
-      set_error("operand %d spans 2 GiB or more", i);
+    if (((tm - 1) * op.stride_m + (tn - 1) * op.stride_n + 1) * (op.dtype == FUSEML_F32 ? 4 : 2) >= kMaxBytes) {
+      set_error("operand %d: one tile's elements span 2 GiB or more", i);
       return FUSEML_EUNSUPPORTED;
     }
   }
@@ -1734,6 +1801,18 @@ int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]) {
   cfg[1] = c.bn;
   cfg[2] = c.wm * c.wn;
   cfg[3] = c.lds_bytes();
+  return FUSEML_OK;
+}
+
+int fuseml_gemm_epilogue_force_variant(const char* name) {
+  g_last_error[0] = '\0';
+  const int v = variant_code(name);
+  if (v < 0) {
+    set_error("unknown variant '%s' (large, deep, deep3, small or auto)", name);
+    return FUSEML_EINVAL;
+  }
+  forced_variant();  // the environment is read first, so it cannot override this later
+  g_forced_variant.store(v, std::memory_order_relaxed);
   return FUSEML_OK;
 }
 

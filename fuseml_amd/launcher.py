@@ -151,6 +151,14 @@ class HipKernelLauncher:
         reds = {name: torch.empty((red_len,), dtype=torch.float32, device=dev) for name in spec.reductions}
 
         if M == 0 or N == 0:
+            # No launch.  A reduction over an empty axis follows torch: sum 0,
+            # mean NaN, amax raises (IndexError, as torch.amax does).
+            reduced_len = N if spec.reduce_axis == 1 else M
+            if red_len > 0 and reduced_len == 0:
+                if "amax" in reds:
+                    raise IndexError("amax(): Expected reduction dim to have non-zero size.")
+                for name, t in reds.items():
+                    t.fill_(0.0 if name == "sum" else float("nan"))
             return self._assemble(tile, extras, reds)
 
         key = (M, N, K, a.stride(0), b.stride(1), tuple((o.stride(), o.dtype) for o in operands))

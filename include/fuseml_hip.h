@@ -33,6 +33,9 @@
  *   - Every call is asynchronous on `stream` and captures no host state, so it
  *     is safe inside HIP graph capture.  Reduction buffers are initialised by a
  *     fill kernel on the same stream (no hipMemset).
+ *   - Operands and outputs may exceed 2 GiB: buffer accesses are based at each
+ *     tile's origin, so only the elements one 256x256 tile reaches must span
+ *     less than 2 GiB.
  *   - Return value: 0 on success, a negative FUSEML_E* code otherwise; the
  *     message is available from fuseml_last_error() on the calling thread.
  */
@@ -155,11 +158,30 @@ int fuseml_gemm_epilogue_supported(const fuseml_gemm_desc* desc);
  * parameter selection of kernel_launcher.py:134-306 / sram_autotuner.py. */
 int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]);
 
+/* Pin the kernel variant for every later launch in this process: "large"
+ * (256x256 ping-pong), "deep" (256x256 one wave per SIMD), "deep3" (the same
+ * with whole-stage fragments; K % 64 == 0, else deep), "small" (128x128), or
+ * NULL / "" / "auto" for the automatic choice.  The environment variable
+ * FUSEML_HIP_TILE sets the initial value; it is read once per process.  For
+ * tuning sweeps and per-variant parity tests; it replaces pinning a Triton
+ * autotune config (fuseml/codegen/kernel_generator.py:587-615).  Returns
+ * FUSEML_EINVAL for an unknown name. */
+int fuseml_gemm_epilogue_force_variant(const char* name);
+
 /* Thread-local text of the last error on this thread ("" if none). */
 const char* fuseml_last_error(void);
 
 /* gcnArchName of `device` (e.g. "gfx950:sramecc+:xnack-") into buf. */
 int fuseml_device_arch(int device, char* buf, int buflen);
+
+/* Measurement only (no reference counterpart; the reference's benchmark
+ * prices against a spec table, benchmarks/bench_mlp_block.py:228-412): launch
+ * `workgroups` workgroups of 4 waves, each wave issuing `iters` x 8 independent
+ * v_mfma_f32_32x32x16_bf16 on random register operands and nothing else, on
+ * `stream`.  FLOPs = workgroups * 4 * iters * 8 * 32768.  `sink` is a device
+ * buffer of workgroups * 256 floats.  Timed by the caller, this is the bf16
+ * MFMA rate the device sustains at its power-limited clock. */
+int fuseml_mfma_peak_probe(int64_t iters, int32_t workgroups, float* sink, void* stream);
 
 /* FUSEML_ABI_VERSION and sizeof(fuseml_gemm_desc), for binding checks. */
 int fuseml_abi_version(void);

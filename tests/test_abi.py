@@ -83,3 +83,39 @@ def test_tile_config_choice():
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(64, 512, 2048)), cfg) == 0
     assert tuple(cfg[:3]) == (128, 128, 4)
     assert 2 * cfg[3] <= 160 * 1024  # two workgroups share one gfx950 CU's LDS
+
+
+def test_force_variant_pins_and_releases():
+    lib = _abi.load_library()
+    cfg = (ctypes.c_int32 * 4)()
+    try:
+        _abi.force_variant("small")
+        assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
+        assert tuple(cfg[:3]) == (128, 128, 4)
+        _abi.force_variant("deep3")
+        assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
+        assert tuple(cfg[:3]) == (256, 256, 4)
+        with pytest.raises(ValueError):
+            _abi.force_variant("huge")
+    finally:
+        _abi.force_variant(None)
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
+    assert tuple(cfg[:3]) == (256, 256, 8)
+
+
+def test_operand_span_limit_is_per_tile():
+    """Buffer accesses are based at each tile's origin: an operand larger than
+    2 GiB is accepted when one tile's elements span less than that."""
+    lib = _abi.load_library()
+    d = _desc(40000, 32768, 64)
+    d.n_operands = 1
+    o = d.operands[0]
+    o.ptr, o.stride_m, o.stride_n, o.dtype = 0x10000, 32768, 1, _abi.BF16
+    o.extent = 40000 * 32768                     # 2.6 GB of bf16
+    d.n_ops = 1
+    d.ops[0].kind, d.ops[0].operand = _abi.OP_ADD, 0
+    assert lib.fuseml_gemm_epilogue_supported(ctypes.byref(d)) == 1, _abi.last_error(lib)
+    o.stride_m = 1 << 23                         # 256 rows of this stride span 4 GiB
+    o.extent = 39999 * (1 << 23) + 32768
+    assert lib.fuseml_gemm_epilogue_supported(ctypes.byref(d)) == 0
+    assert "2 GiB" in _abi.last_error(lib)

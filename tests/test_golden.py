@@ -3,7 +3,8 @@
 CPU tier: the oracle reproduces every fixture.
 GPU tier: the HIP kernel family (one fused launch per group, through the C ABI)
 reproduces the bf16 fixtures within the stated tolerances
-(tiles rtol/atol 2e-2; fp32 reductions 1e-2 relative to the reduction's scale).
+(tiles rtol/atol 2e-2; fp32 reductions 1e-2 of |ref|, floored at 1e-3 of the
+reduction of |v|).
 """
 
 import os
@@ -93,7 +94,8 @@ def _close(got, ref, what):
 
 def _red_close(got, ref, scale, what):
     g = got.float().cpu().numpy().astype(np.float64)
-    assert np.all(np.abs(g - ref) <= 1e-2 * np.maximum(np.abs(ref), scale) + 1e-6), what
+    # 1e-2 of |ref|, floored at 1e-3 of the reduction of |v| (sums that cancel)
+    assert np.all(np.abs(g - ref) <= 1e-2 * np.maximum(np.abs(ref), 1e-3 * scale) + 1e-7), what
 
 
 @pytest.mark.gpu

@@ -4,7 +4,8 @@ Each workload (BASELINE configs C1-C5; M scaled down so the float64 oracle
 stays fast, every other dimension at full size) is compiled, run under
 no_grad, and compared with the CPU oracle on the same bf16 inputs.  The test
 also asserts that the fused HIP launchers actually ran (no silent eager path).
-Tolerances: tiles rtol/atol 2e-2; fp32 reductions 1e-2 of the reduction scale.
+Tolerances: tiles rtol/atol 2e-2; fp32 reductions 1e-2 of |ref| (floored at
+1e-3 of the same reduction of |v|, for sums that cancel).
 """
 
 import numpy as np
@@ -125,7 +126,7 @@ def test_c4_row_reductions_compiled_with_sibling_fusion():
     for got, key, scale in ((s, "sum", a.sum(1)), (mx, "amax", a.max(1)), (mean, "mean", a.mean(1))):
         assert got.dtype == torch.float32
         g = _f64(got)
-        assert np.all(np.abs(g - ref[key]) <= 1e-2 * np.maximum(np.abs(ref[key]), scale) + 1e-6), key
+        assert np.all(np.abs(g - ref[key]) <= 1e-2 * np.maximum(np.abs(ref[key]), 1e-3 * scale) + 1e-7), key
 
 
 def test_c4_default_discovery_matches_reference_grouping():
@@ -234,4 +235,4 @@ def test_3d_broadcast_operands_and_last_dim_reduction():
     v = 1.0 / (1.0 + np.exp(-(_f64(x) @ _f64(m.l2.weight).T + _f64(m.l2.bias))))
     ref_s = v.sum(-1)
     err = np.abs(_f64(s) - ref_s)
-    assert (err <= 1e-2 * np.abs(v).sum(-1) + 1e-3).all(), err.max()
+    assert (err <= 1e-2 * np.maximum(np.abs(ref_s), 1e-3 * np.abs(v).sum(-1))).all(), err.max()

@@ -8,8 +8,10 @@ in float64 on the same (exactly representable) input values.
 Tolerances (stated by the benchmark contract):
   * 16-bit tile outputs: ``allclose(out, ref, rtol=2e-2, atol=2e-2)`` against
     the float64 oracle;
-  * fp32 reductions: ``|red - ref| <= 1e-2 * max(|ref|, ref_abs)`` where
-    ``ref_abs`` is the same reduction of ``|v|`` (the reduction's own scale).
+  * fp32 reductions: ``|red - ref| <= 1e-2 * |ref|``, floored at
+    ``1e-2 * 1e-3 * ref_abs`` where ``ref_abs`` is the same reduction of
+    ``|v|`` (only a sum or mean that cancels to within 0.1% of its scale
+    reaches the floor).
 """
 
 from __future__ import annotations
@@ -26,6 +28,7 @@ pytestmark = pytest.mark.gpu
 RTOL = 2e-2
 ATOL = 2e-2
 RED_RTOL = 1e-2
+RED_FLOOR = 1e-3
 
 
 def _launcher(spec, n_inputs):
@@ -60,7 +63,7 @@ def _check_tile(out: torch.Tensor, ref: np.ndarray, what: str = "tile"):
 def _check_red(out: torch.Tensor, ref: np.ndarray, ref_abs: np.ndarray, what: str):
     got = _np(out)
     assert got.shape == ref.shape, (what, got.shape, ref.shape)
-    tol = RED_RTOL * np.maximum(np.abs(ref), ref_abs) + 1e-6
+    tol = RED_RTOL * np.maximum(np.abs(ref), RED_FLOOR * ref_abs) + 1e-7
     err = np.abs(got - ref)
     assert (err <= tol).all(), f"{what}: max err {err.max()} (tol at worst {tol[err.argmax()]})"
 
@@ -157,7 +160,7 @@ def test_reductions_parity(axis, shape):
 
 # ---------------------------------------------------------------------------
 # Every kernel variant (tile size and K-loop schedule), forced through
-# FUSEML_HIP_TILE, which the library reads at each launch.  The automatic choice
+# _abi.force_variant (FUSEML_HIP_TILE is read once per process).  The automatic choice
 # picks the 256x256 variants only at large sizes, so these cases are what pins
 # the ping-pong ("large") and one-wave-per-SIMD ("deep", "deep3"; BK=64)
 # schedules on every chain, on ragged edges and on K that ends mid-stage.
@@ -182,9 +185,12 @@ VARIANT_SHAPES = [
 
 
 @pytest.fixture
-def forced_variant(request, monkeypatch):
-    monkeypatch.setenv("FUSEML_HIP_TILE", request.param)
-    return request.param
+def forced_variant(request):
+    from fuseml_amd import _abi
+
+    _abi.force_variant(request.param)
+    yield request.param
+    _abi.force_variant(None)
 
 
 @pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)

@@ -204,3 +204,32 @@ def test_nd_operands_and_output_views():
     assert c["operands"][2] == (N, 1, B * S * N, _abi.BF16)
     assert c["operands"][3] == (0, 1, N, _abi.BF16)
     assert out.shape == shape and out.is_contiguous()
+
+
+@pytest.mark.parametrize("axis", [1, 0])
+def test_empty_reduction_axis_matches_torch(axis):
+    """M or N zero: no launch; a reduction over the empty axis is sum 0 and
+    mean NaN, and amax raises IndexError like torch.amax."""
+    rec = Recorder()
+    M, N = (8, 0) if axis == 1 else (0, 8)
+    x, w = torch.randn(M, 16, dtype=BF), torch.randn(N, 16, dtype=BF)
+    spec = EpilogueSpec(0, 1, (EpiOp("relu"),), BF, store_tile=False, reductions=("sum", "mean"),
+                        reduce_axis=axis, reduce_dtypes=(torch.float32,) * 2,
+                        outputs=(("red", "sum"), ("red", "mean")))
+    s, mean = make(spec, 2, rec)(x, w.t())
+    h = torch.relu(x.float() @ w.float().t())
+    assert rec.calls == []
+    assert torch.equal(s, h.sum(axis)) and torch.equal(mean.isnan(), h.mean(axis).isnan())
+    spec_max = EpilogueSpec(0, 1, (EpiOp("relu"),), BF, store_tile=False, reductions=("amax",),
+                            reduce_axis=axis, reduce_dtypes=(torch.float32,), outputs=(("red", "amax"),))
+    with pytest.raises(IndexError):
+        make(spec_max, 2, rec)(x, w.t())
+
+
+def test_empty_rows_give_empty_reductions():
+    rec = Recorder()
+    x, w = torch.randn(0, 16, dtype=BF), torch.randn(8, 16, dtype=BF)
+    spec = EpilogueSpec(0, 1, (EpiOp("relu"),), BF, store_tile=True, reductions=("amax",),
+                        reduce_axis=1, reduce_dtypes=(torch.float32,), outputs=(("tile",), ("red", "amax")))
+    tile, mx = make(spec, 2, rec)(x, w.t())
+    assert tile.shape == (0, 8) and mx.shape == (0,) and rec.calls == []
