@@ -144,11 +144,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
+// IEEE 754-2019 maximum / minimum: NaN if either operand is NaN (torch.amax
+// and torch.clamp semantics; fmaxf / fminf return the other operand).  One
+// v_maximum3_f32 / v_minimum3_f32 each on gfx950.
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float min_nan(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
   // Saturate to the finite fp16 range before narrowing
-  // (fuseml/codegen/kernel_generator.py:1575-1581).
-  // NaN is kept (the clamp alone would turn it into -65504).
-  x = __builtin_isnan(x) ? x : fminf(fmaxf(x, -kFp16Max), kFp16Max);
+  // (fuseml/codegen/kernel_generator.py:1575-1581); NaN stays NaN.
+  x = min_nan(max_nan(x, -kFp16Max), kFp16Max);
   _Float16 h = (_Float16)x;
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
@@ -164,8 +169,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 }
 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
-  a = __builtin_isnan(a) ? a : fminf(fmaxf(a, -kFp16Max), kFp16Max);
-  b = __builtin_isnan(b) ? b : fminf(fmaxf(b, -kFp16Max), kFp16Max);
+  a = min_nan(max_nan(a, -kFp16Max), kFp16Max);
+  b = min_nan(max_nan(b, -kFp16Max), kFp16Max);
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
 }
 
@@ -257,10 +262,6 @@ __device__ __forceinline__ void atomic_max_f32(float* p, float v) {
     atomicMin(reinterpret_cast<unsigned int*>(p), __float_as_uint(v));
 }
 
-// max(a, b), NaN if either is NaN (fmaxf returns the other operand).
-__device__ __forceinline__ float nan_max(float a, float b) {
-  return __builtin_isunordered(a, b) ? __builtin_nanf("") : fmaxf(a, b);
-}
 
 // Standard normal CDF for GELU (approximate='none'):
 //   Phi(x) = 0.5 (1 + erf(x / sqrt 2)) ~= 0.5 + x * Q(x^2)  for |x| <= 3 sqrt 2,
@@ -1154,15 +1155,10 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // chains).  16 instead of 8 for the one-wave schedule measured no faster.
     constexpr int EW = 8;
     const bool out_bf16 = d.out.dtype == FUSEML_BF16;
-    // Row partials (sum, max) of this lane's rows.  The max partial uses fmaxf
-    // (one VALU op per element) and a NaN seen in the row is recorded in rnan,
-    // applied when the partials are combined.
-    float rs[NJ], rmx[NJ];
-    bool rnan[NJ];
+    float rs[NJ], rmx[NJ];  // row partials (sum, max) of this lane's rows
     static_for<0, NJ>([&](auto j) {
       rs[j] = 0.0f;
       rmx[j] = -INFINITY;
-      rnan[j] = false;
     });
     float* red_sum = reinterpret_cast<float*>(smem);
     float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
@@ -1304,11 +1300,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       // output overwrites the staged operand in place: each 8-byte unit is read
       // (above) and written (here) by the same lane.
       float cs[16], cmx[16];
-      bool cnan[16];
       static_for<0, 16>([&](auto r) {
         cs[r] = 0.0f;
         cmx[r] = -INFINITY;
-        cnan[r] = false;
       });
       static_for<0, NJ>([&](auto j) {
         const int m = mw + 32 * j;
@@ -1353,13 +1347,11 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
             const float x = A[j][(int)r];
             if (row_red && in) {
               rs[j] += x;
-              rmx[j] = fmaxf(rmx[j], x);
-              rnan[j] |= __builtin_isnan(x);
+              rmx[j] = max_nan(rmx[j], x);
             }
             if (col_red && in) {
               cs[r] += x;
-              cmx[r] = fmaxf(cmx[r], x);
-              cnan[r] |= __builtin_isnan(x);
+              cmx[r] = max_nan(cmx[r], x);
             }
           });
         }
@@ -1369,11 +1361,10 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         // reductions use neither a staged output nor a staged operand (the host
         // does not flag them), so the staging tile's LDS is free here.
         static_for<0, 16>([&](auto r) {
-          if (cnan[r]) cmx[r] = __builtin_nanf("");
   #pragma unroll
           for (int sh = 1; sh < 32; sh <<= 1) {
             cs[r] += __shfl_xor(cs[r], sh);
-            cmx[r] = nan_max(cmx[r], __shfl_xor(cmx[r], sh));
+            cmx[r] = max_nan(cmx[r], __shfl_xor(cmx[r], sh));
           }
           if (l32 == 0) {
             const int col = wn * TN + 32 * i + 8 * (r >> 2) + 4 * khalf + (r & 3);
@@ -1449,9 +1440,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       if (use_stage_out || staged >= 0) __syncthreads();
       // Row partials: the other half-wave holds the other 4-column runs of the same rows.
       static_for<0, NJ>([&](auto j) {
-        const float m1 = rnan[j] ? __builtin_nanf("") : rmx[j];
         const float s2 = rs[j] + __shfl_xor(rs[j], 32);
-        const float m2 = nan_max(m1, __shfl_xor(m1, 32));
+        const float m2 = max_nan(rmx[j], __shfl_xor(rmx[j], 32));
         if (lane < 32) {
           const int row = wm * TM + 32 * j + lane;
           red_sum[wn * BM + row] = s2;
@@ -1472,7 +1462,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       float s = 0.0f, mx = -INFINITY;
       for (int w = 0; w < nparts; ++w) {
         s += red_sum[w * len + t];
-        mx = nan_max(mx, red_max[w * len + t]);
+        mx = max_nan(mx, red_max[w * len + t]);
       }
       if (d.reduce_mask & FUSEML_RED_SUM) atomicAdd(d.reduce_out[0] + idx, s);
       if (d.reduce_mask & FUSEML_RED_AMAX) atomic_max_f32(d.reduce_out[1] + idx, mx);
