@@ -331,6 +331,23 @@ def _config_detail(name, args, dev, peak_tflops, flush):
         dom = max(kernels, key=lambda k: k["avg_ms"])
         out["dominant_frac_spec"] = dom["frac_spec"]
 
+        if name == "C2":
+            # the opt-in single-kernel MLP block (h kept on chip), same inputs
+            from fuseml_amd.mlp import HipMlpLauncher
+
+            mlp = HipMlpLauncher()
+            m = wl.model
+            margs = (wl.inputs[0], m.linear1.weight.t(), m.linear1.bias, m.linear2.weight.t(), m.linear2.bias,
+                     wl.inputs[0])
+
+            def single():
+                last["mlp"] = mlp(*margs)
+
+            t = _time_events(single, args)
+            t["check"] = _check({"tile": last["mlp"]}, ref, rows)
+            t["tflops"] = round(wl.flops / (t["median_ms"] * 1e-3) / 1e12, 1)
+            t["frac_spec"] = round(t["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)
+            out["fused_mlp_block"] = t
         if not args.no_eager:
             out["eager"] = _time_events(lambda: wl.model(*wl.inputs), args)
             eo = wl.model(*wl.inputs)

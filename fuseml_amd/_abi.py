@@ -17,7 +17,7 @@ import os
 import threading
 from typing import Optional
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_OPS = 16
 MAX_OPERANDS = 8
 MAX_EXTRA_OUT = 4
@@ -72,7 +72,10 @@ EXPORTED_SYMBOLS = (
     "fuseml_device_arch",
     "fuseml_abi_version",
     "fuseml_desc_size",
+    "fuseml_mlp_desc_size",
     "fuseml_mfma_peak_probe",
+    "fuseml_mlp_block",
+    "fuseml_mlp_block_supported",
 )
 
 
@@ -128,6 +131,30 @@ class GemmDesc(ctypes.Structure):
     ]
 
 
+class MlpDesc(ctypes.Structure):
+    """fuseml_mlp_desc: the single-kernel MLP block (y = GELU(x W1^T + b1) W2^T + b2 + r)."""
+
+    _fields_ = [
+        ("M", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("I", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("ldx", ctypes.c_int64),
+        ("w1", ctypes.c_void_p),
+        ("ldw1", ctypes.c_int64),
+        ("b1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("ldw2", ctypes.c_int64),
+        ("b2", ctypes.c_void_p),
+        ("r", ctypes.c_void_p),
+        ("ldr", ctypes.c_int64),
+        ("y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("gelu", ctypes.c_int32),
+    ]
+
+
 class FuseMLHipError(RuntimeError):
     """A non-zero return code from the C ABI (recoverable by the eager guard)."""
 
@@ -162,18 +189,26 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fuseml_abi_version.restype = ctypes.c_int
     lib.fuseml_mfma_peak_probe.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
     lib.fuseml_mfma_peak_probe.restype = ctypes.c_int
+    mlp_p = ctypes.POINTER(MlpDesc)
+    lib.fuseml_mlp_block.argtypes = [mlp_p, ctypes.c_void_p]
+    lib.fuseml_mlp_block.restype = ctypes.c_int
+    lib.fuseml_mlp_block_supported.argtypes = [mlp_p]
+    lib.fuseml_mlp_block_supported.restype = ctypes.c_int
     lib.fuseml_desc_size.argtypes = []
     lib.fuseml_desc_size.restype = ctypes.c_size_t
+    lib.fuseml_mlp_desc_size.argtypes = []
+    lib.fuseml_mlp_desc_size.restype = ctypes.c_size_t
 
 
 def check_abi(lib: ctypes.CDLL) -> None:
     ver = lib.fuseml_abi_version()
-    size = lib.fuseml_desc_size()
-    if ver != ABI_VERSION or size != ctypes.sizeof(GemmDesc):
+    size = lib.fuseml_desc_size() if ver == ABI_VERSION else -1
+    mlp = lib.fuseml_mlp_desc_size() if ver == ABI_VERSION else -1
+    if ver != ABI_VERSION or size != ctypes.sizeof(GemmDesc) or mlp != ctypes.sizeof(MlpDesc):
         raise ImportError(
-            f"{library_path()} ABI mismatch: library v{ver} desc {size} B, "
-            f"binding v{ABI_VERSION} desc {ctypes.sizeof(GemmDesc)} B — rebuild with "
-            "`python -m fuseml_amd.build`"
+            f"{library_path()} ABI mismatch: library v{ver} desc {size} B mlp desc {mlp} B, "
+            f"binding v{ABI_VERSION} desc {ctypes.sizeof(GemmDesc)} B mlp desc {ctypes.sizeof(MlpDesc)} B "
+            "— rebuild with `python -m fuseml_amd.build`"
         )
 
 

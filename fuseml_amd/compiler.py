@@ -185,13 +185,14 @@ class FuseMLCompiler:
     """``torch.compile`` backend fusing addmm/mm epilogue chains into HIP kernels."""
 
     def __init__(self, registry: Any = None, *, fuse_sibling_reductions: bool = False,
-                 fuse_leading_views: bool = False,
+                 fuse_leading_views: bool = False, fuse_mlp_block: bool = False,
                  min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
                  min_tiles_long_k: int = MIN_TILES_LONG_K,
                  require_gfx950: bool = True) -> None:
         self.registry = registry
         self.fuse_sibling_reductions = fuse_sibling_reductions
         self.fuse_leading_views = fuse_leading_views
+        self.fuse_mlp_block = fuse_mlp_block
         self.min_output_elements = min_output_elements
         self.min_tiles_long_k = min_tiles_long_k
         self.require_gfx950 = require_gfx950
@@ -250,6 +251,8 @@ class FuseMLCompiler:
             raise _NoFusionPossible("fusion pass found no fusible sequence")
 
         strategies = set()
+        if self.fuse_mlp_block:
+            placeholders = self._bind_mlp_blocks(gm, placeholders, strategies)
         for ph in placeholders:
             group: FusionGroup = ph.meta["fusion_group"]
             # the pre-scan's verdict (the base node's args are gone after surgery)
@@ -287,6 +290,61 @@ class FuseMLCompiler:
         self.fusion_applied = "hip" in strategies
         self.fusion_strategy = "hip" if strategies == {"hip"} else ("mixed" if self.fusion_applied else "eager")
         return gm.forward
+
+    def _bind_mlp_blocks(self, gm: torch.fx.GraphModule, placeholders: List[torch.fx.Node],
+                         strategies: set) -> List[torch.fx.Node]:
+        """Bind each (GEMM1+bias+GELU, GEMM2+bias+residual) placeholder pair whose
+        GELU output feeds only the second GEMM to one single-kernel MLP launcher
+        (``fuse_mlp_block=True``); return the placeholders left to bind."""
+        from .mlp import HipMlpLauncher, mlp_eager_fn, mlp_first_group, mlp_second_group, mlp_shape_supported
+
+        specs: Dict[torch.fx.Node, Any] = {}
+        for ph in placeholders:
+            try:
+                specs[ph] = spec_from_group(ph.meta["fusion_group"])
+            except UnsupportedGroup:
+                specs[ph] = None
+        used: set = set()
+        for ph2 in placeholders:
+            sp2 = specs.get(ph2)
+            m2 = mlp_second_group(sp2) if sp2 is not None else None
+            if m2 is None:
+                continue
+            ph1 = ph2.args[m2["h"]]
+            if not isinstance(ph1, torch.fx.Node) or ph1 not in specs or ph1 in used or specs[ph1] is None:
+                continue
+            m1 = mlp_first_group(specs[ph1])
+            if m1 is None or list(ph1.users) != [ph2]:
+                continue
+            g1, g2 = ph1.meta["fusion_group"], ph2.meta["fusion_group"]
+            n1, n2 = len(g1.inputs), len(g2.inputs)
+            slots1 = {k: m1[k] for k in ("x", "w1t", "b1")}
+            slots2 = {k: m2[k] for k in ("h", "w2t", "b2", "r")}
+            if sorted(slots1.values()) != list(range(n1)) or sorted(slots2.values()) != list(range(n2)):
+                continue
+            xm, wm, dt = _meta(ph1.args[m1["x"]]), _meta(ph1.args[m1["w1t"]]), specs[ph1].out_dtype
+            if xm is None or wm is None or len(xm.shape) != 2 or len(wm.shape) != 2:
+                continue
+            ok, why = mlp_shape_supported(int(xm.shape[0]), int(xm.shape[1]), int(wm.shape[1]), dt)
+            if not ok:
+                logger.info("MLP pair %s + %s keeps two launches: %s", g1, g2, why)
+                continue
+            eager = mlp_eager_fn(EagerGroupLauncher(g1.eager_module), EagerGroupLauncher(g2.eager_module),
+                                 n1, n2, slots1, slots2)
+            launcher = HipMlpLauncher(m1["approximate"], eager_fn=eager,
+                                      kernel_signature=f"{g1!r} + {g2!r}: mlp_block")
+            args = (ph1.args[m1["x"]], ph1.args[m1["w1t"]], ph1.args[m1["b1"]],
+                    ph2.args[m2["w2t"]], ph2.args[m2["b2"]], ph2.args[m2["r"]])
+            with gm.graph.inserting_after(ph2):
+                new = gm.graph.call_function(launcher, args=args)
+            new.meta.update({k: v for k, v in ph2.meta.items() if k != "fusion_group"})
+            ph2.replace_all_uses_with(new)
+            gm.graph.erase_node(ph2)
+            gm.graph.erase_node(ph1)
+            used.update((ph1, ph2))
+            self.launchers.append(launcher)
+            strategies.add("hip")
+        return [ph for ph in placeholders if ph not in used]
 
     @property
     def cache(self) -> LauncherCache:

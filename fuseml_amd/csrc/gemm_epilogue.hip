@@ -1763,6 +1763,14 @@ int device_cus(int dev) {
 
 }  // namespace
 
+namespace fuseml_detail {
+// Error text for the other translation units of the library (mlp_block.hip).
+void set_error_text(const char* msg) {
+  strncpy(g_last_error, msg, sizeof(g_last_error) - 1);
+  g_last_error[sizeof(g_last_error) - 1] = '\0';
+}
+}  // namespace fuseml_detail
+
 extern "C" {
 
 const char* fuseml_last_error(void) { return g_last_error; }
@@ -1770,6 +1778,8 @@ const char* fuseml_last_error(void) { return g_last_error; }
 int fuseml_abi_version(void) { return FUSEML_ABI_VERSION; }
 
 size_t fuseml_desc_size(void) { return sizeof(fuseml_gemm_desc); }
+
+size_t fuseml_mlp_desc_size(void) { return sizeof(fuseml_mlp_desc); }
 
 int fuseml_gemm_epilogue_supported(const fuseml_gemm_desc* desc) {
   g_last_error[0] = '\0';

@@ -1,0 +1,485 @@
+// mlp_block.hip — the whole MLP block in one kernel: the intermediate
+// activation h never leaves the CU.
+//
+//   h = GELU(x @ W1^T + b1)            x [M, D], W1 [I, D], b1 [I]
+//   y = h @ W2^T + b2 + r               W2 [D, I], b2 [D], r [M, D] (residual)
+//
+// The reference cannot form this group: an addmm ends a group (BARRIER_OPS,
+// fuseml/passes/topology.py:63-64) and absorption needs a single user
+// (fuseml/passes/fusion_pass.py:203-206), so the block is two launches of its
+// generated kernel with h written to and read back from HBM (the two-group
+// module of benchmarks/bench_mlp_block.py:160-182).
+//
+// Structure (one workgroup of 4 waves per CU, persistent over 64-row blocks):
+//   * The row block's y accumulator, 64 x D fp32, stays in AGPRs for the whole
+//     pass over I: wave w owns columns [w D/4, (w+1) D/4) (D <= 1024: at most
+//     256 AGPRs per lane).
+//   * x[64, D] sits in LDS for the row block (XOR-swizzled 16-byte chunks;
+//     fragment reads are free of bank conflicts).
+//   * I is walked in chunks of 32.  For chunk c each wave computes the partial
+//     h[64, 32] over its quarter of D (GEMM1, K split four ways, so each wave
+//     loads a different quarter of the chunk's W1 rows); the four partials meet
+//     in LDS, each thread reduces 8 values, adds b1, applies GELU and writes
+//     h as 16-bit into LDS; then every wave multiplies h by its W2 columns into
+//     its y accumulators (GEMM2).  W1 and W2 fragments go straight from global
+//     memory into registers, one phase ahead (W2 of chunk c during GEMM1 of c,
+//     W1 of chunk c+1 from the end of GEMM1 of c).
+//   * After the last chunk: y + b2 + r, one 16-bit store.
+// MFMA: v_mfma_f32_32x32x16_{bf16,f16}, fp32 accumulation, with the weight
+// rows as MFMA "A" so that each lane holds one output row and runs of four
+// columns (the layout of the GEMM+epilogue kernels).
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <atomic>
+#include <type_traits>
+
+#include "fuseml_hip.h"
+
+namespace fuseml_detail {
+// The library's error text (fuseml_last_error), shared with gemm_epilogue.hip.
+void set_error_text(const char* msg);
+}  // namespace fuseml_detail
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kBM = 64;           // rows per block
+constexpr int kBI = 32;           // intermediate columns per chunk
+constexpr int kThreads = 256;     // 4 waves
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kXBytesMax = kBM * 1024 * 2;            // x tile for D = 1024
+constexpr int kPartBytes = kBM * kBI * 4;             // one wave's fp32 partial h
+constexpr int kLds = kXBytesMax + 4 * kPartBytes;     // 160 KB
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* q = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0x7fffffffLL ? 0x7fffffffu : (uint32_t)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, (int)__builtin_amdgcn_readfirstlane(n), kRsrcWord3);
+}
+
+template <typename T>
+__device__ __forceinline__ f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c);
+
+template <>
+__device__ __forceinline__ f32x16_t mfma32<__bf16>(i32x4_t a, i32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+template <>
+__device__ __forceinline__ f32x16_t mfma32<_Float16>(i32x4_t a, i32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f32(uint32_t h) {
+  if constexpr (std::is_same<T, __bf16>::value)
+    return __uint_as_float(h << 16);
+  else
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+
+template <>
+__device__ __forceinline__ uint32_t pack2<__bf16>(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+template <>
+__device__ __forceinline__ uint32_t pack2<_Float16>(float a, float b) {
+  // fp16 saturation (fuseml/codegen/kernel_generator.py:1575-1581); NaN stays NaN
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  a = __builtin_elementwise_minimum(__builtin_elementwise_maximum(a, -65504.0f), 65504.0f);
+  b = __builtin_elementwise_minimum(__builtin_elementwise_maximum(b, -65504.0f), 65504.0f);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+}
+
+// GELU(erf): x * Phi(x), Phi(x) = 0.5 + xc * Q(xc^2), xc = clamp(x, +-3 sqrt 2);
+// Q is the least-squares fit of erf(z)/z of fuseml_amd/csrc/fit_erf.py (the
+// same coefficients as the GEMM+epilogue kernels; |Phi error| <= 3.3e-5).
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float xc = __builtin_amdgcn_fmed3f(x, -4.2426406871192851f, 4.2426406871192851f);
+  const float t = xc * xc;
+  float q = fmaf(5.955950179e-11f, t, -5.604949355e-09f);
+  q = fmaf(q, t, 2.335694047e-07f);
+  q = fmaf(q, t, -5.748589919e-06f);
+  q = fmaf(q, t, 9.446521791e-05f);
+  q = fmaf(q, t, -1.113571280e-03f);
+  q = fmaf(q, t, 9.828446245e-03f);
+  q = fmaf(q, t, -6.635807263e-02f);
+  q = fmaf(q, t, 3.989064909e-01f);
+  return x * fmaf(xc, q, 0.5f);
+}
+
+// GELU(tanh) = x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3) (Hendrycks &
+// Gimpel 2016), with the hardware exp2 and reciprocal.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  constexpr float kC = 0.79788456080286536f;
+  const float u2 = (2.0f * x) * fmaf(kC * 0.044715f, x * x, kC);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * u2));
+}
+
+// Byte offset of 16-byte chunk q of x row m in the LDS x tile (row pitch 2D
+// bytes): the chunk index is XOR-ed with m & 15, so the 16 consecutive rows
+// one fragment read touches land on 16 distinct bank groups.
+__device__ __forceinline__ int x_chunk(int m, int q, int pitch) { return m * pitch + ((q ^ (m & 15)) << 4); }
+
+// Byte offset of 16-byte chunk q (0..7) of row m of a [64][32] fp32 partial
+// (128-byte rows): XOR with (m >> 1) & 7 spreads 16 consecutive rows over the
+// 16 bank groups, for the accumulator-layout writes and the row reads alike.
+// The 16-bit h tile uses chunk 2j ^ ((m >> 1) & 7) of partial 0's row m for its
+// columns [8j, 8j + 8): the thread that writes it read exactly that chunk.
+__device__ __forceinline__ int part_chunk(int m, int q) { return m * 128 + ((q ^ ((m >> 1) & 7)) << 4); }
+
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8)); }
+
+// Workgroup barrier after this wave's LDS accesses have completed
+// (lgkmcnt(0): an s_barrier alone does not wait for them).  Global loads in
+// flight (the next weight fragments) are not waited for, which
+// __syncthreads()'s fence would do.
+__device__ __forceinline__ void barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// DW: 32-column blocks of y per wave (D = 128 DW).  GELU: FUSEML_OP_GELU_ERF or _TANH.
+template <int DW, int GELU, typename T>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1)))
+void mlp_block_kernel(const fuseml_mlp_desc d) {
+  constexpr int D = 128 * DW;
+  constexpr int PITCH = 2 * D;      // x tile row pitch in bytes
+  constexpr int KS1 = D / 64;       // GEMM1 k-steps per wave (its quarter of D)
+  __shared__ __attribute__((aligned(1024))) char smem[kLds];
+  char* xs = smem;
+  char* part = smem + kXBytesMax;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int kh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = (int)d.M, I = (int)d.I;
+  const int nblocks = (M + kBM - 1) / kBM;
+  const int nchunks = I / kBI;
+
+  const __amdgpu_buffer_rsrc_t rw1 = make_rsrc(d.w1, ((int64_t)(I - 1) * d.ldw1 + D) * 2);
+  const __amdgpu_buffer_rsrc_t rw2 = make_rsrc(d.w2, ((int64_t)(D - 1) * d.ldw2 + I) * 2);
+  const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(d.b1, (int64_t)I * 2);
+
+  // W1 fragment k-step s of this wave, chunk c: row i = 32c + l32, columns
+  // [wave D/4 + 16 s + 8 kh, +8).  W2 fragment (db, s), chunk c: row
+  // d = wave D/4 + 32 db + l32, columns [32 c + 16 s + 8 kh, +8).
+  const uint32_t w1_lane = (uint32_t)l32 * (uint32_t)d.ldw1 * 2u + (uint32_t)(wave * (D / 4) + 8 * kh) * 2u;
+  const uint32_t w1_chunk = (uint32_t)kBI * (uint32_t)d.ldw1 * 2u;
+  const uint32_t w2_lane = (uint32_t)(wave * (D / 4) + l32) * (uint32_t)d.ldw2 * 2u + (uint32_t)(8 * kh) * 2u;
+  const uint32_t w2_dblk = 32u * (uint32_t)d.ldw2 * 2u;
+  i32x4_t w1f[KS1];
+  i32x4_t w2f[DW][2];
+  auto load_w1 = [&](int c) {
+    static_for<0, KS1>([&](auto s) {
+      w1f[s] = __builtin_amdgcn_raw_buffer_load_b128(rw1, w1_lane + (uint32_t)c * w1_chunk + (uint32_t)(32 * s), 0, 0);
+    });
+  };
+  auto load_w2 = [&](int c) {
+    static_for<0, DW>([&](auto db) {
+      static_for<0, 2>([&](auto s) {
+        w2f[db][s] = __builtin_amdgcn_raw_buffer_load_b128(
+            rw2, w2_lane + (uint32_t)db * w2_dblk + (uint32_t)(c * kBI * 2 + 32 * s), 0, 0);
+      });
+    });
+  };
+
+  for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
+    const int m0 = blk * kBM;
+    if (blk != (int)blockIdx.x) barrier();  // the previous block's epilogue no longer reads LDS
+    // The lane index passes through an empty asm each row block, so the x DMA
+    // and epilogue offsets derived from it are recomputed per block rather than
+    // hoisted out of the block loop and held (which spills).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+
+    // x[m0 .. m0+63, :] into LDS by the global -> LDS DMA: one wave-wide
+    // 16-byte DMA fills 1 KB, i.e. 64 physical chunks of a row; the lane whose
+    // slot is physical chunk p of row m fetches logical chunk p ^ (m & 15).
+    // Rows past M read zeros (their results are never stored).
+    {
+      const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(d.x) + (int64_t)m0 * d.ldx * 2,
+                                                  ((int64_t)(M - 1 - m0) * d.ldx + D) * 2);
+      constexpr int kDmas = kBM * PITCH / 1024;  // per workgroup
+      for (int i = wave; i < kDmas; i += 4) {
+        const int byte = i * 1024 + ln * 16;
+        const int m = byte / PITCH;
+        const int p = (byte % PITCH) >> 4;
+        const int q = p ^ (m & 15);
+        const uint32_t off = m0 + m < M ? ((uint32_t)m * (uint32_t)d.ldx + (uint32_t)(8 * q)) * 2u : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + i * 1024),
+                                                 16, off, 0, 0, 0);
+      }
+    }
+    load_w1(0);
+
+    f32x16_t acc[2][DW];
+    static_for<0, 2>([&](auto mb) {
+      static_for<0, DW>([&](auto db) {
+        static_for<0, 16>([&](auto r) { acc[mb][db][(int)r] = 0.0f; });
+      });
+    });
+    wait_vmcnt0();
+    barrier();  // x tile landed
+
+    for (int c = 0; c < nchunks; ++c) {
+      load_w2(c);
+      // GEMM1: partial h over this wave's quarter of D.
+      f32x16_t h1[2];
+      static_for<0, 2>([&](auto mb) { static_for<0, 16>([&](auto r) { h1[mb][(int)r] = 0.0f; }); });
+      static_for<0, KS1>([&](auto s) {
+        const int q = (wave * (D / 4) + 16 * s) / 8 + kh;
+        static_for<0, 2>([&](auto mb) {
+          const int m = 32 * mb + l32;
+          const i32x4_t xf = *reinterpret_cast<const i32x4_t*>(xs + x_chunk(m, q, PITCH));
+          h1[mb] = mfma32<T>(w1f[s], xf, h1[mb]);
+        });
+      });
+      if (c + 1 < nchunks) load_w1(c + 1);
+      // Partials: h1[mb][r] = h[32 mb + l32][8 (r>>2) + 4 kh + (r&3)].
+      barrier();  // every wave's GEMM2 of the previous chunk has read h
+      char* mine = part + wave * kPartBytes;
+      static_for<0, 2>([&](auto mb) {
+        const int m = 32 * mb + l32;
+        static_for<0, 4>([&](auto g) {
+          const f32x4_t v = {h1[mb][4 * g], h1[mb][4 * g + 1], h1[mb][4 * g + 2], h1[mb][4 * g + 3]};
+          *reinterpret_cast<f32x4_t*>(mine + part_chunk(m, 2 * g + kh)) = v;
+        });
+      });
+      barrier();  // partials complete
+      // Reduce: thread t takes row t/4, columns [8 (t%4), +8); bias, GELU, 16-bit h.
+      {
+        const int m = tid >> 2;
+        const int j = tid & 3;
+        float v[8];
+        static_for<0, 8>([&](auto e) { v[e] = 0.0f; });
+        static_for<0, 4>([&](auto p) {
+          const char* src = part + p * kPartBytes;
+          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src + part_chunk(m, 2 * j));
+          const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + part_chunk(m, 2 * j + 1));
+          static_for<0, 4>([&](auto e) {
+            v[e] += a[(int)e];
+            v[4 + e] += b[(int)e];
+          });
+        });
+        const i32x4_t bb = __builtin_amdgcn_raw_buffer_load_b128(rb1, (uint32_t)(c * kBI + 8 * j) * 2u, 0, 0);
+        static_for<0, 4>([&](auto e) {
+          const uint32_t w = (uint32_t)bb[(int)e];
+          v[2 * e] += to_f32<T>(w & 0xffffu);
+          v[2 * e + 1] += to_f32<T>(w >> 16);
+        });
+        static_for<0, 8>([&](auto e) {
+          if constexpr (GELU == FUSEML_OP_GELU_TANH)
+            v[e] = gelu_tanh(v[e]);
+          else
+            v[e] = gelu_erf(v[e]);
+        });
+        const i32x4_t hv = {(int)pack2<T>(v[0], v[1]), (int)pack2<T>(v[2], v[3]), (int)pack2<T>(v[4], v[5]),
+                            (int)pack2<T>(v[6], v[7])};
+        *reinterpret_cast<i32x4_t*>(part + part_chunk(m, 2 * j)) = hv;
+      }
+      barrier();  // h complete
+      // GEMM2: y[64, this wave's D/4 columns] += h[64, 32] W2[:, chunk]^T.
+      static_for<0, 2>([&](auto s) {
+        i32x4_t hf[2];
+        static_for<0, 2>([&](auto mb) {
+          const int m = 32 * mb + l32;
+          hf[mb] = *reinterpret_cast<const i32x4_t*>(part + part_chunk(m, 2 * (2 * s + kh)));
+        });
+        static_for<0, DW>([&](auto db) {
+          static_for<0, 2>([&](auto mb) { acc[mb][db] = mfma32<T>(w2f[db][s], hf[mb], acc[mb][db]); });
+        });
+      });
+    }
+
+    // Epilogue: y = acc + b2 + r, 16-bit.  acc[mb][db][r] is
+    // y[m0 + 32 mb + l32][wave D/4 + 32 db + 8 (r>>2) + 4 kh + (r&3)].  No
+    // branches: an absent b2 or r is a zero-length buffer (its loads read zero),
+    // and rows past M are stored at an out-of-range offset (dropped).
+    const __amdgpu_buffer_rsrc_t rb2 = make_rsrc(d.b2, d.b2 ? (int64_t)D * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(d.r ? static_cast<const char*>(d.r) + (int64_t)m0 * d.ldr * 2 : nullptr,
+                                                d.r ? ((int64_t)(M - 1 - m0) * d.ldr + D) * 2 : 0);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<char*>(d.y) + (int64_t)m0 * d.ldy * 2,
+                                                ((int64_t)(M - 1 - m0) * d.ldy + D) * 2);
+    const int el32 = ln & 31, ekh = ln >> 5;
+    static_for<0, 2>([&](auto mb) {
+      const int ml = 32 * mb + el32;
+      const bool row_ok = m0 + ml < M;
+      static_for<0, DW>([&](auto db) {
+        static_for<0, 4>([&](auto g) {
+          const int col = wave * (D / 4) + 32 * db + 8 * g + 4 * ekh;
+          const i32x2_t b = __builtin_amdgcn_raw_buffer_load_b64(rb2, (uint32_t)col * 2u, 0, 0);
+          const i32x2_t rv = __builtin_amdgcn_raw_buffer_load_b64(
+              rr, row_ok ? ((uint32_t)ml * (uint32_t)d.ldr + (uint32_t)col) * 2u : kOOB, 0, 0);
+          float y[4];
+          static_for<0, 4>([&](auto e) {
+            const uint32_t bw = (uint32_t)(e < 2 ? b.x : b.y) >> (16 * (e & 1));
+            const uint32_t rw = (uint32_t)(e < 2 ? rv.x : rv.y) >> (16 * (e & 1));
+            y[e] = acc[mb][db][4 * g + e] + to_f32<T>(bw & 0xffffu) + to_f32<T>(rw & 0xffffu);
+          });
+          const i32x2_t out = {(int)pack2<T>(y[0], y[1]), (int)pack2<T>(y[2], y[3])};
+          __builtin_amdgcn_raw_buffer_store_b64(
+              out, ry, row_ok ? ((uint32_t)ml * (uint32_t)d.ldy + (uint32_t)col) * 2u : kOOB, 0, 0);
+        });
+      });
+    });
+  }
+}
+
+void set_error(const char* msg) { fuseml_detail::set_error_text(msg); }
+
+// gfx950 check and CU count, queried once per device.
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
+
+int device_cus(int dev) {
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int known = g_cus[dev].load(std::memory_order_relaxed);
+    if (known != 0) return known;
+  }
+  char arch[64] = {0};
+  int cus = 0;
+  if (fuseml_device_arch(dev, arch, sizeof(arch)) != FUSEML_OK) return FUSEML_EHIP;
+  if (strncmp(arch, "gfx950", 6) != 0) {
+    set_error("mlp_block: kernels are built for gfx950 only");
+    return FUSEML_EDEVICE;
+  }
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    set_error("hipDeviceGetAttribute(MultiprocessorCount) failed");
+    return FUSEML_EHIP;
+  }
+  if (dev >= 0 && dev < kMaxDevices) g_cus[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+int validate(const fuseml_mlp_desc* dp) {
+  if (dp == nullptr) {
+    set_error("null descriptor");
+    return FUSEML_EINVAL;
+  }
+  const fuseml_mlp_desc& d = *dp;
+  if (d.M <= 0 || d.D <= 0 || d.I <= 0 || d.x == nullptr || d.w1 == nullptr || d.b1 == nullptr ||
+      d.w2 == nullptr || d.y == nullptr) {
+    set_error("empty problem or missing operand");
+    return FUSEML_EINVAL;
+  }
+  if (d.dtype != FUSEML_BF16 && d.dtype != FUSEML_F16) {
+    set_error("mlp_block: bf16/f16 only");
+    return FUSEML_EUNSUPPORTED;
+  }
+  if (d.gelu != FUSEML_OP_GELU_ERF && d.gelu != FUSEML_OP_GELU_TANH) {
+    set_error("mlp_block: activation must be GELU (erf or tanh)");
+    return FUSEML_EINVAL;
+  }
+  if (!(d.D == 256 || d.D == 512 || d.D == 1024)) {
+    set_error("mlp_block: D must be 256, 512 or 1024 (the 64 x D accumulator lives in registers)");
+    return FUSEML_EUNSUPPORTED;
+  }
+  if (d.I % 32 != 0 || d.M >= ((int64_t)1 << 30) || d.I >= ((int64_t)1 << 24)) {
+    set_error("mlp_block: I must be a multiple of 32");
+    return FUSEML_EUNSUPPORTED;
+  }
+  if (d.ldx < d.D || d.ldw1 < d.D || d.ldw2 < d.I || d.ldy < d.D || (d.r && d.ldr < d.D) || d.ldx % 8 ||
+      d.ldw1 % 8 || d.ldw2 % 8 || d.ldy % 4 || (d.r && d.ldr % 4) || ((uintptr_t)d.x & 15) ||
+      ((uintptr_t)d.w1 & 15) || ((uintptr_t)d.w2 & 15) || ((uintptr_t)d.b1 & 15) || ((uintptr_t)d.y & 7) ||
+      (d.b2 && ((uintptr_t)d.b2 & 7)) || (d.r && ((uintptr_t)d.r & 7))) {
+    set_error("mlp_block: strides or alignment not supported");
+    return FUSEML_EUNSUPPORTED;
+  }
+  // 32-bit buffer offsets: the weights are addressed whole, x and r per row block.
+  const int64_t lim = (int64_t)1 << 31;
+  if (((d.I - 1) * d.ldw1 + d.D) * 2 >= lim || ((d.D - 1) * d.ldw2 + d.I) * 2 >= lim ||
+      (int64_t)kBM * d.ldx * 2 >= lim || (d.r && (int64_t)kBM * d.ldr * 2 >= lim)) {
+    set_error("mlp_block: an operand spans 2 GiB or more");
+    return FUSEML_EUNSUPPORTED;
+  }
+  return FUSEML_OK;
+}
+
+template <int DW, typename T>
+hipError_t launch_dw(const fuseml_mlp_desc& d, int grid, hipStream_t s) {
+  if (d.gelu == FUSEML_OP_GELU_TANH)
+    hipLaunchKernelGGL((mlp_block_kernel<DW, FUSEML_OP_GELU_TANH, T>), dim3(grid), dim3(kThreads), 0, s, d);
+  else
+    hipLaunchKernelGGL((mlp_block_kernel<DW, FUSEML_OP_GELU_ERF, T>), dim3(grid), dim3(kThreads), 0, s, d);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_t(const fuseml_mlp_desc& d, int grid, hipStream_t s) {
+  switch (d.D) {
+    case 256: return launch_dw<2, T>(d, grid, s);
+    case 512: return launch_dw<4, T>(d, grid, s);
+    default: return launch_dw<8, T>(d, grid, s);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int fuseml_mlp_block_supported(const fuseml_mlp_desc* desc) {
+  set_error("");
+  return validate(desc) == FUSEML_OK ? 1 : 0;
+}
+
+int fuseml_mlp_block(const fuseml_mlp_desc* desc, void* stream) {
+  set_error("");
+  const int rc = validate(desc);
+  if (rc != FUSEML_OK) return rc;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("hipGetDevice failed");
+    return FUSEML_EHIP;
+  }
+  const int cus = device_cus(dev);
+  if (cus <= 0) return cus < 0 ? cus : FUSEML_EHIP;
+  const int64_t nblocks = (desc->M + kBM - 1) / kBM;
+  const int grid = (int)(nblocks < cus ? nblocks : cus);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const hipError_t e = desc->dtype == FUSEML_BF16 ? launch_t<__bf16>(*desc, grid, s) : launch_t<_Float16>(*desc, grid, s);
+  if (e != hipSuccess) {
+    set_error("mlp_block launch failed");
+    return FUSEML_EHIP;
+  }
+  return FUSEML_OK;
+}
+
+}  // extern "C"

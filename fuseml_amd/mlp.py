@@ -1,0 +1,169 @@
+"""The single-kernel MLP block: two fusion groups in one launch.
+
+The reference forms two groups for ``linear2(gelu(linear1(x))) + x`` — an
+addmm ends a group (fuseml/passes/topology.py:63-64) and absorption needs a
+single user (fuseml/passes/fusion_pass.py:203-206) — so the GELU output ``h``
+is written to HBM by the first launch and read back by the second.  With
+``FuseMLCompiler(fuse_mlp_block=True)`` a pair of groups
+
+    G1: addmm(b1, x, t(W1)) -> gelu                      (h has one user: G2)
+    G2: addmm(b2, h, t(W2)) -> add(., r)
+
+is bound to one :class:`HipMlpLauncher`, which calls ``fuseml_mlp_block``:
+``h`` stays in LDS chunk by chunk and never reaches HBM.  The kernel holds a
+64 x D fp32 accumulator per row block in registers, so it takes D (the model
+width) of 256, 512 or 1024 only; other pairs keep their two launches.
+
+The launcher's calling convention is the fused launchers' (``__name__``,
+positional inputs, ``ValueError`` on arity, fresh row-major output, launch on
+the current stream with no host synchronisation) with the inputs
+``(x, t(W1), b1, t(W2), b2, r)``; its eager fallback runs the two groups'
+original nodes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Any, Callable, Dict, Optional, Tuple
+
+import torch
+
+from . import _abi
+from .epilogue import EpilogueSpec
+from .fallback import EagerFallbackGuard
+
+MLP_WIDTHS = (256, 512, 1024)
+MLP_CHUNK = 32
+
+_DTYPES = {torch.bfloat16: _abi.BF16, torch.float16: _abi.F16}
+
+
+def mlp_shape_supported(M: int, D: int, I: int, dtype: torch.dtype) -> Tuple[bool, str]:
+    """Host-side restatement of the kernel's shape limits (for the cost model)."""
+    if dtype not in _DTYPES:
+        return False, f"dtype {dtype}: bf16/f16 only"
+    if D not in MLP_WIDTHS:
+        return False, f"D={D}: the 64 x D accumulator fits registers for D in {MLP_WIDTHS} only"
+    if I % MLP_CHUNK != 0:
+        return False, f"I={I} is not a multiple of {MLP_CHUNK}"
+    if M <= 0:
+        return False, "empty batch"
+    return True, "fused"
+
+
+class HipMlpLauncher:
+    """Callable ``(x, t(W1), b1, t(W2), b2, r) -> y`` on ``fuseml_mlp_block``."""
+
+    N_INPUTS = 6
+
+    def __init__(self, approximate: str = "none", eager_fn: Optional[Callable[..., Any]] = None,
+                 kernel_signature: str = "mlp_block") -> None:
+        self.__name__ = "fuseml_mlp_block"
+        self.approximate = approximate
+        self._gelu = _abi.OP_GELU_TANH if approximate == "tanh" else _abi.OP_GELU_ERF
+        self._lib = _abi.load_library()
+        self._desc = _abi.MlpDesc()
+        self._guard = EagerFallbackGuard(eager_fn, kernel_signature) if eager_fn is not None else None
+        self.launch_count = 0
+
+    @property
+    def fallback_count(self) -> int:
+        return self._guard.fallback_count if self._guard else 0
+
+    def __repr__(self) -> str:
+        return f"HipMlpLauncher(gelu={self.approximate})"
+
+    def launch(self, x: torch.Tensor, w1t: torch.Tensor, b1: torch.Tensor, w2t: torch.Tensor,
+               b2: Optional[torch.Tensor], r: Optional[torch.Tensor]) -> torch.Tensor:
+        if x.dim() != 2 or w1t.dim() != 2 or w2t.dim() != 2:
+            raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "mlp_block takes 2-D x and weights")
+        M, D = x.shape
+        I = w1t.shape[1]
+        dt = x.dtype
+        if dt not in _DTYPES or any(t is not None and t.dtype != dt for t in (w1t, b1, w2t, b2, r)):
+            raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "mlp_block: every tensor must share one bf16/f16 dtype")
+        if tuple(w1t.shape) != (D, I) or tuple(w2t.shape) != (I, D) or b1.shape != (I,) or \
+                (b2 is not None and b2.shape != (D,)) or (r is not None and tuple(r.shape) != (M, D)):
+            raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "mlp_block: operand shapes do not chain")
+        # K-contiguous operands (the graph's layouts: x row-major, t(W) views).
+        if x.stride(1) != 1:
+            x = x.contiguous()
+        if w1t.stride(0) != 1:
+            w1t = w1t.t().contiguous().t()
+        if w2t.stride(0) != 1:
+            w2t = w2t.t().contiguous().t()
+        b1 = b1.contiguous()
+        if b2 is not None:
+            b2 = b2.contiguous()
+        if r is not None and r.stride(1) != 1:
+            r = r.contiguous()
+        y = torch.empty((M, D), dtype=dt, device=x.device)
+        if M == 0:
+            return y
+        d = self._desc
+        d.M, d.D, d.I = M, D, I
+        d.x, d.ldx = x.data_ptr(), x.stride(0)
+        d.w1, d.ldw1 = w1t.data_ptr(), w1t.stride(1)
+        d.b1 = b1.data_ptr()
+        d.w2, d.ldw2 = w2t.data_ptr(), w2t.stride(1)
+        d.b2 = b2.data_ptr() if b2 is not None else None
+        d.r, d.ldr = (r.data_ptr(), r.stride(0)) if r is not None else (None, D)
+        d.y, d.ldy = y.data_ptr(), D
+        d.dtype = _DTYPES[dt]
+        d.gelu = self._gelu
+        stream = torch.cuda.current_stream(x.device).cuda_stream if x.device.type == "cuda" else 0
+        rc = self._lib.fuseml_mlp_block(ctypes.byref(d), ctypes.c_void_p(stream))
+        if rc != _abi.OK:
+            raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
+        self.launch_count += 1
+        return y
+
+    def __call__(self, *inputs: Any) -> torch.Tensor:
+        if len(inputs) != self.N_INPUTS:
+            raise ValueError(f"Expected {self.N_INPUTS} inputs (x, t(W1), b1, t(W2), b2, r), got {len(inputs)}.")
+        if self._guard is not None:
+            return self._guard.execute(lambda: self.launch(*inputs), inputs)
+        return self.launch(*inputs)
+
+
+# ---------------------------------------------------------------------------
+# Group-pair matching (compile time)
+# ---------------------------------------------------------------------------
+
+
+def mlp_first_group(spec: EpilogueSpec) -> Optional[Dict[str, Any]]:
+    """G1 = addmm(b1, x, t(W1)) -> gelu: the slots of b1/x/t(W1) and the GELU form."""
+    if spec.reductions or spec.extra_dtypes or not spec.store_tile or len(spec.ops) != 2 \
+            or spec.output_shapes or spec.operand_shapes:
+        return None
+    bias, act = spec.ops
+    if bias.kind != "add" or bias.scalar != 1.0 or act.kind not in ("gelu_erf", "gelu_tanh"):
+        return None
+    return {"x": spec.left, "w1t": spec.right, "b1": bias.operand,
+            "approximate": "tanh" if act.kind == "gelu_tanh" else "none"}
+
+
+def mlp_second_group(spec: EpilogueSpec) -> Optional[Dict[str, Any]]:
+    """G2 = addmm(b2, h, t(W2)) -> add(., r): the slots of h/t(W2)/b2/r."""
+    if spec.reductions or spec.extra_dtypes or not spec.store_tile or len(spec.ops) != 2 \
+            or spec.output_shapes or spec.operand_shapes:
+        return None
+    bias, res = spec.ops
+    if bias.kind != "add" or bias.scalar != 1.0 or res.kind != "add" or res.scalar != 1.0:
+        return None
+    return {"h": spec.left, "w2t": spec.right, "b2": bias.operand, "r": res.operand}
+
+
+def mlp_eager_fn(g1_fn: Callable[..., Any], g2_fn: Callable[..., Any], n1: int, n2: int,
+                 slots1: Dict[str, int], slots2: Dict[str, int]) -> Callable[..., Any]:
+    """The two groups' eager closures chained, with the launcher's input order."""
+
+    def run(x, w1t, b1, w2t, b2, r):
+        a1 = [None] * n1
+        a1[slots1["x"]], a1[slots1["w1t"]], a1[slots1["b1"]] = x, w1t, b1
+        h = g1_fn(*a1)
+        a2 = [None] * n2
+        a2[slots2["h"]], a2[slots2["w2t"]], a2[slots2["b2"]], a2[slots2["r"]] = h, w2t, b2, r
+        return g2_fn(*a2)
+
+    return run

@@ -16,6 +16,15 @@ dispatches in issue order and groups dispatch i as launch i % N.
 device-to-device copy of known size run in the same process
 (``bench.py --calib-copy-mb``): factor = copy bytes / counter bytes.
 
+``mfma-busy`` turns one counter pass of ``SQ_VALU_MFMA_BUSY_CYCLES`` and
+``GRBM_GUI_ACTIVE`` into the MFMA-busy fraction of each launch: the ratio of
+the two counters, divided by the same ratio read for the MFMA-only probe
+(``fuseml_mfma_peak_probe``, which ``bench.py`` runs in the same process and
+which keeps every SIMD's MFMA pipe busy), so the normalisation (counter
+aggregation over XCDs, CUs and SIMDs) cancels.  It also reports each launch's
+clock, GRBM_GUI_ACTIVE per XCD over the traced duration when a kernel trace
+of the same run is given.
+
 ``step-traffic`` sums the same counters over every dispatch of a run (the
 calibration copy aside) and divides by ``--calls``, the number of times the
 run called the module (``bench.py --eager-only`` prints it): HBM bytes per
@@ -33,6 +42,7 @@ from collections import defaultdict
 from typing import Dict, List, Tuple
 
 COPY_KERNEL_HINT = "copyBuffer"
+PROBE_KERNEL_HINT = "mfma_peak_kernel"
 
 
 def _short(name: str) -> str:
@@ -114,6 +124,28 @@ def traffic_summary(fetch_csv: str, write_csv: str, copy_mib: float, per_step: i
     return {"copy_mib": copy_mib, "fetch_factor": ff, "write_factor": wf, "kernels": kernels}
 
 
+def mfma_busy_summary(pmc_csv: str, per_step: int = 1, xcds: int = 8) -> Dict[str, object]:
+    busy = counter_by_dispatch(pmc_csv, "SQ_VALU_MFMA_BUSY_CYCLES", per_step)
+    gui = counter_by_dispatch(pmc_csv, "GRBM_GUI_ACTIVE", per_step)
+    ratio = {k: statistics.mean(busy[k]) / statistics.mean(gui[k]) for k in busy if k in gui and
+             statistics.mean(gui[k]) > 0}
+    probe = [r for (n, _, _), r in ratio.items() if PROBE_KERNEL_HINT in n]
+    ref = statistics.median(probe) if probe else None
+    kernels = []
+    for key in sorted(ratio):
+        name, grid, p = key
+        if COPY_KERNEL_HINT in name:
+            continue
+        kernels.append({
+            "kernel": "mfma_peak_kernel (probe)" if PROBE_KERNEL_HINT in name else _short(name),
+            "grid": grid, "launch": p, "dispatches": len(busy[key]),
+            "mfma_busy_cycles": statistics.mean(busy[key]), "grbm_gui_active": statistics.mean(gui[key]),
+            "gui_active_per_xcd": statistics.mean(gui[key]) / xcds,
+            "mfma_busy_frac": None if ref is None else round(ratio[key] / ref, 4),
+        })
+    return {"probe_ratio": ref, "kernels": kernels}
+
+
 def step_traffic(fetch_csv: str, write_csv: str, copy_mib: float, calls: int) -> Dict[str, object]:
     """HBM bytes per call of a whole module (every dispatch but the calibration
     copy), for a run that called the module ``calls`` times: totals over the
@@ -158,6 +190,9 @@ def main(argv=None) -> int:
     tr.add_argument("write_csv")
     tr.add_argument("--copy-mib", type=float, required=True)
     tr.add_argument("--per-step", type=int, default=1)
+    mb = sub.add_parser("mfma-busy")
+    mb.add_argument("csv")
+    mb.add_argument("--per-step", type=int, default=1)
     st = sub.add_parser("step-traffic")
     st.add_argument("fetch_csv")
     st.add_argument("write_csv")
@@ -169,6 +204,8 @@ def main(argv=None) -> int:
             print(json.dumps(row))
     elif a.cmd == "traffic":
         print(json.dumps(traffic_summary(a.fetch_csv, a.write_csv, a.copy_mib, a.per_step), indent=1))
+    elif a.cmd == "mfma-busy":
+        print(json.dumps(mfma_busy_summary(a.csv, a.per_step), indent=1))
     else:
         print(json.dumps(step_traffic(a.fetch_csv, a.write_csv, a.copy_mib, a.calls), indent=1))
     return 0

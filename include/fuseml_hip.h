@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FUSEML_ABI_VERSION 1
+#define FUSEML_ABI_VERSION 2
 
 #define FUSEML_MAX_OPS 16
 #define FUSEML_MAX_OPERANDS 8
@@ -174,6 +174,46 @@ const char* fuseml_last_error(void);
 /* gcnArchName of `device` (e.g. "gfx950:sramecc+:xnack-") into buf. */
 int fuseml_device_arch(int device, char* buf, int buflen);
 
+/* ------------------------------------------------------------------------
+ * The whole MLP block in one launch (opt-in):
+ *
+ *     y = GELU(x W1^T + b1) W2^T + b2 + r
+ *
+ * with h = GELU(x W1^T + b1) kept on chip (never written to HBM).  The
+ * reference has no counterpart: it runs the block as two launches of its
+ * generated kernel (kernel_launcher.py:793-796 / 811-814, once per group),
+ * because an addmm ends a fusion group (fuseml/passes/topology.py:63-64) and
+ * absorption needs a single user (fuseml/passes/fusion_pass.py:203-206).
+ * Operand layouts are the graph's: x [M,D] row-major; W1 as t(W1) [D,I]
+ * (element (k,i) at w1[i*ldw1 + k]); W2 as t(W2) [I,D] (element (i,d) at
+ * w2[d*ldw2 + i]); b1 [I], b2 [D] (may be NULL), r [M,D] (may be NULL), y [M,D].
+ * Limits: D in {256, 512, 1024} (the 64 x D fp32 accumulator of a row block
+ * lives in registers), I a multiple of 32, all tensors bf16 or all fp16.
+ * ------------------------------------------------------------------------ */
+typedef struct fuseml_mlp_desc {
+  int64_t M, D, I;
+  const void* x;
+  int64_t ldx;
+  const void* w1;
+  int64_t ldw1;
+  const void* b1;
+  const void* w2;
+  int64_t ldw2;
+  const void* b2;
+  const void* r;
+  int64_t ldr;
+  void* y;
+  int64_t ldy;
+  int32_t dtype; /* FUSEML_BF16 | FUSEML_F16, for every tensor     */
+  int32_t gelu;  /* FUSEML_OP_GELU_ERF | FUSEML_OP_GELU_TANH       */
+} fuseml_mlp_desc;
+
+/* Launch the single-kernel MLP block on `stream`.  0 or a FUSEML_E* code. */
+int fuseml_mlp_block(const fuseml_mlp_desc* desc, void* stream);
+
+/* 1 if fuseml_mlp_block accepts `desc`, 0 if not (reason in fuseml_last_error()). */
+int fuseml_mlp_block_supported(const fuseml_mlp_desc* desc);
+
 /* Measurement only (no reference counterpart; the reference's benchmark
  * prices against a spec table, benchmarks/bench_mlp_block.py:228-412): launch
  * `workgroups` workgroups of 4 waves, each wave issuing `iters` x 8 independent
@@ -183,9 +223,11 @@ int fuseml_device_arch(int device, char* buf, int buflen);
  * MFMA rate the device sustains at its power-limited clock. */
 int fuseml_mfma_peak_probe(int64_t iters, int32_t workgroups, float* sink, void* stream);
 
-/* FUSEML_ABI_VERSION and sizeof(fuseml_gemm_desc), for binding checks. */
+/* FUSEML_ABI_VERSION, sizeof(fuseml_gemm_desc) and sizeof(fuseml_mlp_desc),
+ * for binding checks. */
 int fuseml_abi_version(void);
 size_t fuseml_desc_size(void);
+size_t fuseml_mlp_desc_size(void);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,115 @@
+"""GPU parity of the single-kernel MLP block (``fuseml_mlp_block``) against the
+float64 oracle.
+
+``y = GELU(x W1^T + b1) W2^T + b2 + r`` with ``h`` kept on chip.  The kernel
+rounds ``h`` to the operand dtype before the second GEMM, as the two-launch
+path (and eager bf16) do.  Cases: every supported width D (256, 512, 1024),
+ragged M (not a multiple of the 64-row block), I down to one 32-column chunk,
+GELU erf and tanh, bf16 and fp16, no bias/residual, and the C2 config at full
+size through the launcher and through ``FuseMLCompiler(fuse_mlp_block=True)``.
+
+Tolerance: ``allclose(rtol=2e-2, atol=2e-2)`` against the float64 oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm_epilogue as ora
+from oracle import workloads as ora_w
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _close(got, ref, what):
+    g = _np(got)
+    assert g.shape == ref.shape, (what, g.shape, ref.shape)
+    bad = ~np.isclose(g, ref, rtol=2e-2, atol=2e-2)
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} mismatches, max err {np.abs(g - ref).max()}"
+
+
+def _inputs(M, D, I, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, D, generator=g).to(dtype)
+    w1 = (torch.randn(I, D, generator=g) / D ** 0.5).to(dtype)
+    b1 = (torch.rand(I, generator=g) * 0.2 - 0.1).to(dtype)
+    w2 = (torch.randn(D, I, generator=g) / I ** 0.5).to(dtype)
+    b2 = (torch.rand(D, generator=g) * 0.2 - 0.1).to(dtype)
+    r = torch.randn(M, D, generator=g).to(dtype)
+    return x, w1, b1, w2, b2, r
+
+
+def _oracle(x, w1, b1, w2, b2, r, approximate="none", dtype=None):
+    h = ora_w.linear(_np(x), _np(w1), _np(b1))
+    h = ora.gelu_tanh(h) if approximate == "tanh" else ora.gelu_erf(h)
+    y = ora_w.linear(h, _np(w2), None if b2 is None else _np(b2))
+    return y if r is None else y + _np(r)
+
+
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+@pytest.mark.parametrize("shape", [(300, 256, 1024), (129, 512, 96), (64, 1024, 32), (1, 256, 64), (200, 1024, 2048)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_mlp_block_parity(shape, approximate):
+    from fuseml_amd.mlp import HipMlpLauncher
+
+    M, D, I = shape
+    print(f"case mlp_block shape={shape} gelu={approximate}", flush=True)
+    x, w1, b1, w2, b2, r = _inputs(M, D, I, torch.bfloat16, seed=M + D + I)
+    y = HipMlpLauncher(approximate)(x.cuda(), w1.t().cuda(), b1.cuda(), w2.t().cuda(), b2.cuda(), r.cuda())
+    torch.cuda.synchronize()
+    _close(y, _oracle(x, w1, b1, w2, b2, r, approximate), f"mlp_block {shape} {approximate}")
+
+
+def test_mlp_block_fp16_without_bias_and_residual():
+    from fuseml_amd.mlp import HipMlpLauncher
+
+    M, D, I = 257, 512, 512
+    print("case mlp_block fp16 no b2/r", flush=True)
+    x, w1, b1, w2, _, _ = _inputs(M, D, I, torch.float16, seed=5)
+    y = HipMlpLauncher()(x.cuda(), w1.t().cuda(), b1.cuda(), w2.t().cuda(), None, None)
+    torch.cuda.synchronize()
+    _close(y, _oracle(x, w1, b1, w2, None, None), "mlp_block fp16")
+
+
+def test_mlp_block_c2_full_size_launcher():
+    from fuseml_amd.mlp import HipMlpLauncher
+    from fuseml_amd.workloads import c2_mlp_block
+
+    print("case mlp_block C2 full size", flush=True)
+    wl = c2_mlp_block()
+    m, x = wl.model, wl.inputs[0]
+    W1, b1, W2, b2 = m.linear1.weight, m.linear1.bias, m.linear2.weight, m.linear2.bias
+    xd = x.cuda()
+    y = HipMlpLauncher()(xd, W1.t().cuda(), b1.cuda(), W2.t().cuda(), b2.cuda(), xd)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(9)
+    rows = np.unique(np.concatenate([[0, 16383], rng.integers(0, 16384, 64)]))
+    ref = ora_w.transformer_mlp(_np(x), _np(W1), _np(b1), _np(W2), _np(b2), rows=rows)
+    _close(y[torch.as_tensor(rows).cuda()], ref, "C2 mlp_block")
+
+
+def test_mlp_block_compiled_c2():
+    from fuseml_amd.compiler import FuseMLCompiler
+    from fuseml_amd.mlp import HipMlpLauncher
+    from fuseml_amd.workloads import c2_mlp_block
+
+    print("case mlp_block compiled C2 (scale 1/8)", flush=True)
+    wl = c2_mlp_block(scale=1 / 8)
+    m, x = wl.model, wl.inputs[0]
+    ref = ora_w.transformer_mlp(_np(x), _np(m.linear1.weight), _np(m.linear1.bias),
+                                _np(m.linear2.weight), _np(m.linear2.bias))
+    wl.to("cuda")
+    torch._dynamo.reset()
+    be = FuseMLCompiler(fuse_mlp_block=True)
+    with torch.no_grad():
+        y = torch.compile(wl.model, backend=be)(*wl.inputs)
+    torch.cuda.synchronize()
+    (L,) = be.launchers
+    assert isinstance(L, HipMlpLauncher) and L.launch_count == 1 and L.fallback_count == 0
+    _close(y, ref, "compiled mlp_block")

@@ -1,0 +1,120 @@
+"""The single-kernel MLP block's host side on the CPU (no kernel launch).
+
+* ``FuseMLCompiler(fuse_mlp_block=True)`` binds the two groups of
+  ``linear2(gelu(linear1(x))) + x`` to one ``HipMlpLauncher`` (default: the
+  reference's two groups); the launch is forced onto its eager fallback, which
+  chains the two groups' original nodes, so the compiled module equals eager.
+* The launcher fills ``fuseml_mlp_desc`` from the graph's layouts.
+* The shape rule mirrors the kernel's limits.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+import fuseml_amd.compiler as comp
+from fuseml_amd import _abi
+from fuseml_amd.compiler import FuseMLCompiler
+from fuseml_amd.fallback import FORCE_FAIL_ENV
+from fuseml_amd.mlp import HipMlpLauncher, mlp_shape_supported
+from fuseml_amd.workloads import StackedMLP, TransformerMLP
+
+BF = torch.bfloat16
+
+
+def _compile(model, be):
+    torch._dynamo.reset()
+    return torch.compile(model, backend=be)
+
+
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_mlp_block_opt_in_binds_one_launcher(monkeypatch, approximate):
+    torch.manual_seed(0)
+    m = TransformerMLP(256, 1024, approximate=approximate).to(BF).eval()
+    x = torch.randn(64, 256, dtype=BF)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0, fuse_mlp_block=True)
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+        ref = m(x)
+    assert torch.equal(out, ref)
+    assert len(be.launchers) == 1 and isinstance(be.launchers[0], HipMlpLauncher)
+    assert be.launchers[0].approximate == approximate and be.launchers[0].fallback_count == 1
+
+
+def test_mlp_block_off_by_default_keeps_two_groups(monkeypatch):
+    torch.manual_seed(0)
+    m = TransformerMLP(256, 1024).to(BF).eval()
+    x = torch.randn(64, 256, dtype=BF)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+    assert torch.equal(out, m(x))
+    assert len(be.launchers) == 2 and not any(isinstance(l, HipMlpLauncher) for l in be.launchers)
+
+
+def test_mlp_block_stacked_blocks_each_one_launcher(monkeypatch):
+    torch.manual_seed(1)
+    m = StackedMLP(512, 1024, 3).to(BF).eval()
+    x = torch.randn(32, 512, dtype=BF)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0, fuse_mlp_block=True)
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+    assert torch.equal(out, m(x))
+    assert len(be.launchers) == 3 and all(isinstance(l, HipMlpLauncher) for l in be.launchers)
+
+
+def test_unsupported_width_keeps_two_launches(monkeypatch):
+    """D = 768 is not a width the kernel holds in registers: two launches."""
+    torch.manual_seed(0)
+    m = TransformerMLP(768, 1024).to(BF).eval()
+    x = torch.randn(64, 768, dtype=BF)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0, fuse_mlp_block=True)
+    with torch.no_grad():
+        assert torch.equal(_compile(m, be)(x), m(x))
+    assert len(be.launchers) == 2
+
+
+class _Recorder:
+    def __init__(self):
+        self.calls = []
+
+    def fuseml_mlp_block(self, desc_ref, stream):
+        d = ctypes.cast(desc_ref, ctypes.POINTER(_abi.MlpDesc)).contents
+        self.calls.append({f: getattr(d, f) for f, _ in _abi.MlpDesc._fields_})
+        return 0
+
+    def fuseml_last_error(self):
+        return b""
+
+
+def test_mlp_descriptor_from_graph_layouts():
+    M, D, I = 48, 256, 1024
+    x = torch.randn(M, D, dtype=BF)
+    w1, b1 = torch.randn(I, D, dtype=BF), torch.randn(I, dtype=BF)
+    w2, b2 = torch.randn(D, I, dtype=BF), torch.randn(D, dtype=BF)
+    L = HipMlpLauncher("tanh")
+    rec = _Recorder()
+    L._lib = rec
+    y = L(x, w1.t(), b1, w2.t(), b2, x)
+    (c,) = rec.calls
+    assert y.shape == (M, D) and y.dtype == BF
+    assert (c["M"], c["D"], c["I"], c["ldx"], c["ldw1"], c["ldw2"], c["ldr"], c["ldy"]) == (M, D, I, D, D, I, D, D)
+    assert c["x"] == x.data_ptr() and c["r"] == x.data_ptr() and c["w1"] == w1.data_ptr()
+    assert c["dtype"] == _abi.BF16 and c["gelu"] == _abi.OP_GELU_TANH
+    with pytest.raises(ValueError):
+        L(x, w1.t(), b1)
+    with pytest.raises(_abi.FuseMLHipError):   # shapes that do not chain
+        L(x, w1.t(), b1, w1.t(), b2, x)
+
+
+def test_mlp_shape_rule():
+    assert mlp_shape_supported(16384, 1024, 4096, BF)[0]
+    assert mlp_shape_supported(64, 256, 32, torch.float16)[0]
+    assert not mlp_shape_supported(8192, 4096, 16384, BF)[0]      # C5: D too wide
+    assert not mlp_shape_supported(64, 512, 100, BF)[0]           # I % 32
+    assert not mlp_shape_supported(64, 512, 1024, torch.float32)[0]
