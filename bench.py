@@ -410,7 +410,7 @@ def _mfma_busy(workload, launch):
     if data is None:
         return None
     for k in data.get("kernels", []):
-        if k.get("launch") == launch:
+        if str(k.get("kernel", "")).startswith("gemm_epilogue_kernel") and k.get("launch") == launch:
             return k.get("mfma_busy_frac")
     return None
 

@@ -43,3 +43,12 @@ def test_hbm_traffic_from_committed_summaries():
     c5 = b._hbm_traffic("C5", [[8192, 16384, 4096], [8192, 4096, 16384]] * 4)
     assert c5["fused_write_bytes"] == 4 * (8192 * 16384 * 2 + 8192 * 4096 * 2)
     assert b._hbm_traffic("nope", [[1, 1, 1]]) is None
+
+
+def test_mfma_busy_from_committed_summaries():
+    b = _bench()
+    for w, launches in (("C2", 2), ("C3", 1), ("C4", 1), ("C5", 8)):
+        for i in range(launches):
+            f = b._mfma_busy(w, i)
+            assert f is not None and 0.1 < f < 1.0, (w, i, f)
+    assert b._mfma_busy("nope", 0) is None
