@@ -24,8 +24,9 @@ The cost model (replacing topology.py:479-571's NVIDIA tables and the
 Triton/cuBLAS/bypass split) is two-way: the fused HIP kernel when the device
 is gfx950, the operands are bf16/f16, the group fits one launch and its output
 has at least ``min_output_elements`` (the reference's tiny-output rule,
-fusion_pass.py:463 and 498: M*N < 500 000 bypasses), and the GEMM is not a
-few-tile problem with a long K loop, else eager.  The last rule is measured on
+fusion_pass.py:463 and 498: M*N < 500 000 bypasses), the GEMM is not a
+few-tile problem with a long K loop, and the epilogue saves more than the K
+loop gives up against hipBLASLt (:func:`fused_beats_eager`), else eager.  The last rule is measured on
 MI355X (bias+GELU chains against eager addmm + GELU): with K >= 2048 and fewer
 128x128 output tiles than the 256 CUs, each CU runs one tile's whole K loop
 while hipBLASLt's stream-K kernel splits K, and the fused kernel runs at
@@ -53,6 +54,9 @@ logger = logging.getLogger("fuseml_amd")
 MIN_FUSION_OUTPUT_ELEMENTS = 500_000
 LONG_K = 2048
 MIN_TILES_LONG_K = 256  # 128x128 output tiles; MI355X has 256 CUs
+# Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the
+# eager path would run over the [M,N] output): measured crossover on MI355X.
+K_PER_EPILOGUE_PASS = 1024
 SUPPORTED_GEMM_DTYPES = (torch.bfloat16, torch.float16)
 
 
@@ -79,6 +83,20 @@ def device_is_gfx950(device: Optional[torch.device] = None) -> bool:
     except Exception:  # pragma: no cover - no device
         return False
     return str(arch).startswith("gfx950")
+
+
+def _gemm_k(group: Any) -> Optional[int]:
+    """K of the group's GEMM from the left operand's metadata (None if unknown)."""
+    base = group.base_node
+    args = (getattr(group, "node_args_snapshot", None) or {}).get(base.name, base.args)
+    mat1 = args[1] if base.target is TRIGGER_TARGETS[0] else args[0]
+    m = _meta(mat1)
+    if m is None or len(m.shape) != 2:
+        return None
+    try:
+        return int(m.shape[1])
+    except (TypeError, ValueError):
+        return None
 
 
 def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
@@ -141,6 +159,45 @@ def group_eager_fn(group: Any) -> Optional[Callable[..., Any]]:
         return None
 
 
+def epilogue_passes(spec: EpilogueSpec) -> int:
+    """Elementwise passes over the [M,N] result that eager PyTorch runs after
+    the GEMM for this group: every epilogue op except the addmm's own bias /
+    alpha / beta (hipBLASLt applies those in its GEMM epilogue) and the escape
+    stores, plus one read per reduction."""
+    ops = list(spec.ops)
+    # the addmm's own terms come first: scale (alpha), then the bias (add of
+    # a broadcast vector or scalar)
+    i = 0
+    if i < len(ops) and ops[i].kind == "scale":
+        i += 1
+    if i < len(ops) and ops[i].kind in ("add", "add_scalar"):
+        i += 1
+    passes = sum(1 for o in ops[i:] if o.kind != "store")
+    return passes + len(spec.reductions)
+
+
+def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOGUE_PASS) -> Tuple[bool, str]:
+    """The fused kernel against eager (hipBLASLt GEMM + elementwise kernels).
+
+    Measured on one MI355X, each fused group against its eager ops (same box,
+    HIP events): the fused kernel saves one HBM round trip of the [M,N] result
+    per elementwise pass, while its K loop is slower than hipBLASLt's plain
+    GEMM by about a fifth from K = 4096 on (plain GEMM 16384x1024x4096:
+    0.091 ms against the fused 0.126 ms with bias + residual; eager 0.107).
+    With one pass the fused kernel wins at K = 1024 (bias + GELU, 16384x4096:
+    0.159 against eager 0.167 ms) and loses at K = 4096 (8192x16384: 0.874
+    against 0.829 ms) and K = 16384 (bias + residual: 0.801 against 0.714 ms);
+    with four passes it wins at K = 1024 (C3: 0.201 against 0.313 ms) and
+    K = 2048 (ReLU + three row reductions: 0.269 against 0.374 ms).  Rule: fuse
+    iff K <= k_per_pass * passes; k_per_pass = 0 always fuses."""
+    if k_per_pass <= 0:
+        return True, "fused"
+    passes = epilogue_passes(spec)
+    if K <= k_per_pass * passes:
+        return True, "fused"
+    return False, f"K={K} with {passes} elementwise pass(es): eager's GEMM is faster (crossover K <= {k_per_pass} per pass)"
+
+
 def build_hip_launcher(group: Any, eager_fn: Optional[Callable[..., Any]] = None, *,
                        spec: Optional[EpilogueSpec] = None, eager_if_unsupported: bool = True):
     """FusionGroup -> launcher: replaces compiler.py:443-585 (``_build_launcher``)
@@ -188,6 +245,7 @@ class FuseMLCompiler:
                  fuse_leading_views: bool = False, fuse_mlp_block: bool = False,
                  min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
                  min_tiles_long_k: int = MIN_TILES_LONG_K,
+                 k_per_epilogue_pass: int = K_PER_EPILOGUE_PASS,
                  require_gfx950: bool = True) -> None:
         self.registry = registry
         self.fuse_sibling_reductions = fuse_sibling_reductions
@@ -195,6 +253,7 @@ class FuseMLCompiler:
         self.fuse_mlp_block = fuse_mlp_block
         self.min_output_elements = min_output_elements
         self.min_tiles_long_k = min_tiles_long_k
+        self.k_per_epilogue_pass = k_per_epilogue_pass
         self.require_gfx950 = require_gfx950
         self.fusion_candidates: List[torch.fx.Node] = []
         self.fusion_applied: bool = False
@@ -264,6 +323,12 @@ class FuseMLCompiler:
                 except UnsupportedGroup as exc:
                     logger.info("group %s stays eager: %s", group, exc)
                     spec = None
+                if spec is not None:
+                    K = _gemm_k(group)
+                    win, why = fused_beats_eager(spec, K, self.k_per_epilogue_pass) if K else (True, "fused")
+                    if not win:
+                        logger.info("group %s stays eager: %s", group, why)
+                        spec = None
                 key = launcher_cache_key(group, spec) if spec is not None else None
                 launcher = self._cache.lookup(key) if key is not None else None
                 if launcher is None and spec is not None:

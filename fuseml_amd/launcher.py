@@ -63,6 +63,19 @@ def _k_major_right(b: torch.Tensor) -> torch.Tensor:
     return b.t().contiguous().t()
 
 
+def _distinct_bytes(tensors: Sequence[torch.Tensor]) -> int:
+    """Bytes of each distinct tensor (by storage span) counted once: what a launch
+    must move at least (inputs read once, outputs written once)."""
+    seen, total = set(), 0
+    for t in tensors:
+        if isinstance(t, torch.Tensor):
+            key = (t.data_ptr(), t.numel())
+            if key not in seen:
+                seen.add(key)
+                total += t.numel() * t.element_size()
+    return total
+
+
 class HipKernelLauncher:
     """Callable that runs one fused group on the gfx950 kernel family."""
 
@@ -84,6 +97,10 @@ class HipKernelLauncher:
                 eager_fn=eager_fn, kernel_signature=kernel_signature or spec.describe()
             )
         self.launch_count = 0
+        # Measurement hook: a list to receive, per launch, (start event, end
+        # event, (M, N, K), algorithmic bytes) recorded on the launch stream
+        # around the C call.  None (the default) records nothing.
+        self.timing_events: Optional[List[Tuple[Any, Any, Tuple[int, int, int], int]]] = None
 
     # ------------------------------------------------------------------
     @property
@@ -203,9 +220,17 @@ class HipKernelLauncher:
         d.reduce_axis = spec.reduce_axis
 
         stream = torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0
+        timing = self.timing_events
+        if timing is not None:
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
         rc = self._lib.fuseml_gemm_epilogue(ctypes.byref(d), ctypes.c_void_p(stream))
         if rc != _abi.OK:
             raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
+        if timing is not None:
+            ev1.record()
+            outs = [t for t in [tile, *extras, *reds.values()] if t is not None]
+            timing.append((ev0, ev1, (M, N, K), _distinct_bytes([*inputs, *outs])))
         self.launch_count += 1
         return self._assemble(tile, extras, reds)
 

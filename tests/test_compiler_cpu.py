@@ -200,3 +200,37 @@ def test_cache_key_separates_return_signatures(recorded):
     outs = sorted(r.spec.outputs for r in recorded.built)
     assert outs == sorted([(("red", "sum"), ("red", "amax")),
                            (("red", "sum"), ("red", "amax"), ("tile",))])
+
+
+def test_epilogue_passes_and_crossover_rule():
+    """The measured crossover: fuse iff K <= 1024 x (elementwise passes eager
+    would run after the GEMM).  The benchmark configs' groups land on the
+    measured side of it."""
+    from fuseml_amd.compiler import epilogue_passes, fused_beats_eager
+    from fuseml_amd.epilogue import EpilogueSpec, EpiOp
+
+    g1 = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("gelu_erf")), BF)
+    g2 = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("add", 3)), BF)
+    c3 = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("relu"), EpiOp("mul", 3), EpiOp("sigmoid"), EpiOp("add", 4)), BF)
+    c4 = EpilogueSpec(0, 1, (EpiOp("relu"),), BF, reductions=("sum", "amax", "mean"))
+    alpha = EpilogueSpec(1, 2, (EpiOp("scale", scalar=0.5), EpiOp("add", 0), EpiOp("store", 0), EpiOp("relu")), BF)
+    assert [epilogue_passes(s) for s in (g1, g2, c3, c4, alpha)] == [1, 1, 4, 4, 1]
+    assert fused_beats_eager(g1, 1024)[0] and fused_beats_eager(c3, 1024)[0] and fused_beats_eager(c4, 2048)[0]
+    assert not fused_beats_eager(g2, 4096)[0] and not fused_beats_eager(g1, 4096)[0]
+    assert not fused_beats_eager(g2, 16384)[0]
+    assert fused_beats_eager(g2, 16384, k_per_pass=0)[0]
+
+
+def test_long_k_groups_route_to_eager(recorded):
+    """StackedMLP at K = 4096 / 16384 (C5's widths, few rows): every group has
+    one elementwise pass, so the default cost model keeps them eager."""
+    from fuseml_amd.workloads import StackedMLP
+
+    torch.manual_seed(0)
+    m = StackedMLP(4096, 16384, 1).to(BF).eval()
+    x = torch.randn(64, 4096, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False, min_tiles_long_k=0)
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+    assert torch.allclose(out.float(), m(x).float(), atol=1e-2)
+    assert recorded.built == [] and be.fusion_strategy == "eager"

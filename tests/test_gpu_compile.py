@@ -26,9 +26,10 @@ def _compile(model, **kw):
 
     torch._dynamo.reset()
     # The workloads are scaled down (fewer output tiles than CUs at K >= 2048 for
-    # some GEMMs), where the cost model would route to eager: keep the fused
-    # kernels under test.
+    # some GEMMs), and the long-K groups lose to eager's GEMM, so the cost
+    # model would route them to eager: keep the fused kernels under test.
     kw.setdefault("min_tiles_long_k", 0)
+    kw.setdefault("k_per_epilogue_pass", 0)  # long-K groups would route to eager
     be = FuseMLCompiler(**kw)
     return torch.compile(model, backend=be), be
 
