@@ -79,6 +79,9 @@ def _parse():
     p.add_argument("--eager-only", action="store_true",
                    help="run only the eager leg of --workload (rocprof counter runs of the eager module)")
     p.add_argument("--cpu-iters", type=int, default=5)
+    p.add_argument("--settle-s", type=float, default=0.5,
+                   help="untimed seconds of the step before its warm-up steps (the clock ramps up "
+                        "over the first ~100 ms of load)")
     p.add_argument("--all-hip-headline", action="store_true",
                    help="time the all-HIP pipeline as the headline and skip the compiled module "
                         "(rocprof runs of the fused kernels alone)")
@@ -554,9 +557,21 @@ def _calib_copy(mb, dev):
     del src, dst
 
 
-def _run_eager(wl, warmup, steps):
+def _settle(fn, seconds):
+    """Run fn() untimed for `seconds` (then synchronise): the device's clock rises
+    over the first ~100 ms of sustained load, which would otherwise fall into
+    the first timed steps."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+def _run_eager(wl, warmup, steps, settle_s=0.0):
     """The workload's module under PyTorch eager: (forward calls made, ms per timed call)."""
     with torch.no_grad():
+        _settle(lambda: wl.model(*wl.inputs), settle_s)
         n_warm = max(3, warmup)
         for _ in range(n_warm):
             wl.model(*wl.inputs)
@@ -619,6 +634,7 @@ def main():
             compiled(*wl.inputs)
             torch.cuda.synchronize()
             compile_s = time.perf_counter() - t0
+            _settle(lambda: compiled(*wl.inputs), args.settle_s)
             for _ in range(args.warmup):
                 compiled(*wl.inputs)
             torch.cuda.synchronize()
@@ -652,12 +668,13 @@ def main():
         torch._dynamo.reset()
     headline_eager = None
     if not args.no_eager:
-        _, headline_eager = _run_eager(wl, args.warmup, args.steps)
+        _, headline_eager = _run_eager(wl, args.warmup, args.steps, args.settle_s)
 
     # ---- the all-HIP pipeline (every group on the fused kernels), K timed steps ----
     stages = _build_pipeline(name, wl)
     with torch.no_grad():
         state = _initial_state(name, wl)
+        _settle(lambda: _run_pipeline(stages, dict(state)), args.settle_s)
         for _ in range(args.warmup):
             _run_pipeline(stages, dict(state))
         torch.cuda.synchronize()
@@ -722,6 +739,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": args.settle_s,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": False,
         "scaling": "weak",
