@@ -348,6 +348,37 @@ def test_variant_persistent_rounds(forced_variant, shape, axis):
     _check_red(mean, ref["mean"], np.abs(v).mean(axis=axis), "mean")
 
 
+@pytest.mark.parametrize("forced_variant", ["large"], indirect=True)
+@pytest.mark.parametrize("shape,resid", [
+    ((4392, 4360, 264), True),    # 324 tiles (plain order), K ends mid-stage: 9 stages
+    ((3996, 5112, 256), True),    # 320 tiles (XCD order), exactly 2 x 4 stages
+    ((6000, 6100, 512), False),   # 576 tiles: up to three per workgroup, no staged operand
+    ((4392, 4360, 224), True),    # 7 stages
+], ids=["324tiles-k264", "320tiles-k256", "576tiles-bias-gelu", "324tiles-k224"])
+def test_variant_persistent_rounds_staged_output(forced_variant, shape, resid):
+    """The ping-pong schedule over more tiles than workgroups with a staged
+    output and no reductions: ragged M and N, one to three tiles per
+    workgroup, K from 7 to 16 stages, with and without the DMA-staged residual."""
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=51)
+    bias = (torch.rand(N, generator=_gen(52)) - 0.5).to(dtype)
+    inputs = [bias]
+    steps = [("add", 0, 1.0)]
+    if resid:
+        inputs.append(torch.randn(M, N, generator=_gen(53)).to(dtype))
+        steps.append(("add", 1, 1.0))
+    steps.append(("gelu_erf", -1, 1.0))
+    inputs += [a, w.t()]
+    left, right = len(inputs) - 2, len(inputs) - 1
+    spec = _spec(left=left, right=right, ops=steps, out_dtype=dtype)
+    print(f"case variant={forced_variant} persistent staged output shape={shape} resid={resid}", flush=True)
+    out = _launcher(spec, len(inputs))(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], left, right, steps)["tile"]
+    _check_tile(out, ref, f"persistent staged output {shape}")
+
+
 def test_escape_store_and_tile_with_reductions():
     """mm -> relu (escapes) -> row sum/amax/mean: the C4 group shape, small."""
     M, N, K = 320, 640, 256
