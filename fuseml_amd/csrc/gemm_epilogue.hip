@@ -522,12 +522,25 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     // Vector operands with an LDS slot (bias and the like): this thread's element
     // of each is loaded now, lands during the K loop, and is written to its slot
     // (as fp32) after it.  Every slot holds at most one element per thread.
+    // Slot q's load goes straight into aux_bits[q] (q a compile-time index; the
+    // operand holding the slot is found by a scalar search).  Loaded into a
+    // temporary and moved to its slot's register by a runtime choice, the
+    // move would wait for the load, i.e. for its full latency, right here.
     static_assert(AUXLEN <= NT, "one staged vector element per thread");
     uint32_t aux_bits[kAuxSlots];
-    static_for<0, kAuxSlots>([&](auto q) { aux_bits[q] = 0; });
-    for (int oi = 0; oi < d.n_operands; ++oi) {
-      const int fl = d.operands[oi].reserved;
-      if (!(fl & kFlagAux)) continue;
+    static_for<0, kAuxSlots>([&](auto q) {
+      int oi = -1;
+      for (int k = 0; k < d.n_operands; ++k) {
+        const int fl = d.operands[k].reserved;
+        if ((fl & kFlagAux) && ((fl >> 8) & (kAuxSlots - 1)) == q) {
+          oi = k;
+          break;
+        }
+      }
+      if (oi < 0) {
+        aux_bits[q] = 0;
+        return;
+      }
       const bool rowv = d.operands[oi].stride_m == 0;
       const int idx = (rowv ? n0 : m0) + tid;
       const bool ok = tid < (rowv ? BN : BM) && idx < (rowv ? N : M);
@@ -536,13 +549,9 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       const __amdgpu_buffer_rsrc_t r = make_rsrc_at(d.operands[oi].ptr, (int64_t)(rowv ? n0 : m0) * st * eb,
                                                     d.operands[oi].extent * eb);
       const uint32_t off = ok ? (uint32_t)((int64_t)tid * st * eb) : kOOB;
-      const uint32_t bits = (eb == 4) ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)
-                                      : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-      const int slot = (fl >> 8) & (kAuxSlots - 1);
-      static_for<0, kAuxSlots>([&](auto q) {
-        if (slot == q) aux_bits[q] = bits;
-      });
-    }
+      aux_bits[q] = (eb == 4) ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)
+                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    });
 
     // The epilogue stages the first LDS-eligible 2-D operand of the chain in an
     // LDS tile [BM][BN] of 16-bit elements that reuses the pipeline's slots.
