@@ -1575,14 +1575,14 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
   // to stay busy; below one full wave of 256-tile work the 128x128 variant
   // fills more CUs.  Of the 256x256 schedules, the one-wave-per-SIMD ones have
   // the faster K loop but the slower epilogue (no second wave on a SIMD to
-  // overlap its latencies).  The whole-stage one wins from K = 2048 when each
-  // CU runs several tiles (C4 2%, C5 4-10%) or from K = 8192; with a single
-  // round of tiles at K = 4096 (C2's second GEMM: 256 tiles, a residual) its
-  // exposed epilogue loses 0-5%, and at K = 1024 it loses 7-19%.  With
-  // K % 64 != 0 the two-stage one takes over from K = 8192.
+  // overlap its latencies).  The whole-stage one wins from K = 2048 with at
+  // least one full round of tiles (C4 2%, C5 4-10%, C2's second GEMM at K =
+  // 4096 and 256 tiles 3%) or from K = 8192; at K = 1024 it loses 12-16% on
+  // bias+GELU and C3's chain and ties without ops.  With K % 64 != 0 the
+  // two-stage one takes over from K = 8192.
   const int64_t large_tiles = cdiv(d.M, 256) * cdiv(d.N, 256);
   if (large_tiles < 128) return kSmall;
-  if (d.K % 64 == 0 && (d.K >= 8192 || (d.K >= 2048 && large_tiles > cus))) return kDeep3;
+  if (d.K % 64 == 0 && (d.K >= 8192 || (d.K >= 2048 && large_tiles >= cus))) return kDeep3;
   return d.K >= 8192 ? kDeep : kLarge;
 }
 

@@ -452,6 +452,9 @@ def _sample_rows(M, n=48, seed=0):
 
 
 def test_c2_full_size_sampled_rows():
+    """C2 at full size: G1 (K=1024, 1024 tiles) on the ping-pong schedule over
+    four rounds, G2 (K=4096, 256 tiles, residual) on the one-wave whole-stage
+    schedule, one tile per workgroup."""
     from fuseml_amd.workloads import c2_mlp_block
 
     wl = c2_mlp_block()
