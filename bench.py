@@ -65,7 +65,7 @@ RED_RTOL = 1e-2
 def _parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default="C2", choices=sorted(WORKLOAD_DESC), help="headline workload")
     p.add_argument("--configs", default="C2,C3,C4,C5",
@@ -641,6 +641,8 @@ def main():
             hip = list({id(x): x for x in be.launchers if isinstance(x, HipKernelLauncher)}.values())
             for L in hip:
                 L.timing_events = []
+                L.timing_pool = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                                 for _ in range(4 * args.steps)]
             t0 = time.perf_counter()
             for _ in range(args.steps):
                 compiled(*wl.inputs)

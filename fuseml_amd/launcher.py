@@ -76,6 +76,22 @@ def _distinct_bytes(tensors: Sequence[torch.Tensor]) -> int:
     return total
 
 
+class _Plan:
+    """What a launch needs that depends only on the input signature (shapes,
+    strides, dtypes): the descriptor with every non-pointer field filled, M/N/K,
+    and for each operand slot the input it comes from and whether it must be
+    rebuilt per call (a dtype conversion or a broadcast that merging copies)."""
+
+    __slots__ = ("desc", "M", "N", "K", "neg", "operands", "nbytes")
+
+    def __init__(self) -> None:
+        self.desc = _abi.GemmDesc()
+        self.M = self.N = self.K = 0
+        self.neg = False
+        self.operands: List[Tuple[int, bool]] = []  # (input index, rebuilt per call)
+        self.nbytes: Optional[int] = None  # algorithmic bytes, for the timing hook
+
+
 class HipKernelLauncher:
     """Callable that runs one fused group on the gfx950 kernel family."""
 
@@ -90,7 +106,7 @@ class HipKernelLauncher:
         self.spec = spec
         self._n_inputs = n_inputs
         self._lib = _abi.load_library()
-        self._descs: Dict[tuple, _abi.GemmDesc] = {}
+        self._plans: Dict[tuple, _Plan] = {}
         self._fallback_guard: Optional[EagerFallbackGuard] = None
         if eager_fn is not None:
             self._fallback_guard = EagerFallbackGuard(
@@ -99,8 +115,13 @@ class HipKernelLauncher:
         self.launch_count = 0
         # Measurement hook: a list to receive, per launch, (start event, end
         # event, (M, N, K), algorithmic bytes) recorded on the launch stream
-        # around the C call.  None (the default) records nothing.
+        # around the C call.  None (the default) records nothing.  Pairs of
+        # timing events taken from `timing_pool` (filled by the caller before
+        # a timed region) keep event creation out of that region.
         self.timing_events: Optional[List[Tuple[Any, Any, Tuple[int, int, int], int]]] = None
+        self.timing_pool: List[Tuple[Any, Any]] = []
+        # Input slots the launch reads: the GEMM operands and the epilogue operands.
+        self._used = sorted({spec.left, spec.right} | {op.operand for op in spec.ops if op.kind in ("add", "mul")})
 
     # ------------------------------------------------------------------
     @property
@@ -111,44 +132,37 @@ class HipKernelLauncher:
         return f"HipKernelLauncher({self.spec.describe()})"
 
     # ------------------------------------------------------------------
-    def _operand_tensors(self, inputs: Sequence[torch.Tensor], M: int, N: int) -> List[torch.Tensor]:
-        """Broadcast every add/mul operand to a zero-stride [M,N] view.
+    def _operand_tensor(self, t: torch.Tensor, op_index: int, M: int, N: int) -> torch.Tensor:
+        """An add/mul operand as a zero-stride-broadcast [M,N] view.
 
         An operand of an op on an N-D value ([*lead, N], same memory order as
         [M,N]) is broadcast to that shape first and its leading dimensions
         merged; when their strides do not merge (e.g. [B,1,N] against
         [B,S,N]) the merge materialises the broadcast (a copy, still exact).
         """
-        shapes = dict(self.spec.operand_shapes)
-        seen: Dict[int, int] = {}
-        ops: List[torch.Tensor] = []
+        if t.dtype not in _DTYPE_CODE:
+            t = t.to(torch.float32)
+        shape = dict(self.spec.operand_shapes).get(op_index)
+        if shape is not None:
+            return t.expand(shape).reshape(M, N)
+        if t.dim() > 2:
+            raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "operand rank > 2")
+        return t.expand(M, N)
+
+    def _operand_order(self) -> List[int]:
+        """Input index of each operand slot (first-use order, deduplicated)."""
+        order: List[int] = []
         for op in self.spec.ops:
-            if op.kind in ("add", "mul") and op.operand not in seen:
-                t = inputs[op.operand]
-                if t.dtype not in _DTYPE_CODE:
-                    t = t.to(torch.float32)
-                shape = shapes.get(op.operand)
-                if shape is not None:
-                    t = t.expand(shape).reshape(M, N)
-                elif t.dim() > 2:
-                    raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "operand rank > 2")
-                else:
-                    t = t.expand(M, N)
-                seen[op.operand] = len(ops)
-                ops.append(t)
-        self._operand_slot = seen
-        return ops
+            if op.kind in ("add", "mul") and op.operand not in order:
+                order.append(op.operand)
+        return order
 
-    def _desc(self, key: tuple) -> _abi.GemmDesc:
-        d = self._descs.get(key)
-        if d is None:
-            d = _abi.GemmDesc()
-            self._descs[key] = d
-        return d
-
-    def launch(self, *inputs: torch.Tensor) -> Any:
-        """Allocate outputs, fill the descriptor and call the C ABI."""
+    def _make_plan(self, inputs: Sequence[torch.Tensor]) -> _Plan:
         spec = self.spec
+        plan = _Plan()
+        plan.neg = any(_has_negative_stride(inputs[i]) for i in self._used if isinstance(inputs[i], torch.Tensor))
+        if plan.neg:
+            inputs = tuple(t.contiguous() if isinstance(t, torch.Tensor) else t for t in inputs)
         a = _k_major_left(inputs[spec.left])
         b = _k_major_right(inputs[spec.right])
         if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
@@ -157,13 +171,66 @@ class HipKernelLauncher:
             )
         M, K = int(a.shape[0]), int(a.shape[1])
         N = int(b.shape[1])
+        plan.M, plan.N, plan.K = M, N, K
+        d = plan.desc
+        d.M, d.N, d.K = M, N, K
+        d.ab_dtype = _dtype_code(a.dtype)
+        order = self._operand_order()
+        slot = {idx: i for i, idx in enumerate(order)}
+        d.n_ops = len(spec.ops)
+        if d.n_ops > _abi.MAX_OPS:
+            raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "too many epilogue ops")
+        for i, op in enumerate(spec.ops):
+            e = d.ops[i]
+            e.kind = _abi.OP_CODES[op.kind]
+            e.operand = slot[op.operand] if op.kind in ("add", "mul") else op.operand
+            e.scalar = op.scalar
+        d.n_operands = len(order)
+        if d.n_operands > _abi.MAX_OPERANDS:
+            raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "too many epilogue operands")
+        for i, idx in enumerate(order):
+            src = inputs[idx]
+            t = self._operand_tensor(src, idx, M, N)
+            o = d.operands[i]
+            sm, sn = t.stride()
+            o.stride_m, o.stride_n = sm, sn
+            o.extent = (M - 1) * sm + (N - 1) * sn + 1
+            o.dtype = _DTYPE_CODE[t.dtype]
+            # A view of the input itself needs only its pointer per call.
+            direct = t.dtype == src.dtype and t.data_ptr() == src.data_ptr() and \
+                t.untyped_storage().data_ptr() == src.untyped_storage().data_ptr()
+            plan.operands.append((idx, not direct))
+        d.out.ld, d.out.dtype = N, _dtype_code(spec.out_dtype) if spec.store_tile else _abi.BF16
+        d.n_extra = len(spec.extra_dtypes)
+        for i, dt in enumerate(spec.extra_dtypes):
+            d.extra[i].ld, d.extra[i].dtype = N, _dtype_code(dt)
+        mask = 0
+        for name in spec.reductions:
+            mask |= _abi.RED_BITS[name]
+        d.reduce_mask = mask
+        d.reduce_axis = spec.reduce_axis
+        return plan
+
+    def launch(self, *inputs: torch.Tensor) -> Any:
+        """Allocate outputs, set the descriptor's pointers and call the C ABI."""
+        spec = self.spec
+        key = tuple((t.shape, t.stride(), t.dtype) if isinstance(t, torch.Tensor) else None
+                    for t in (inputs[i] for i in self._used))
+        plan = self._plans.get(key)
+        if plan is None:
+            plan = self._make_plan(inputs)
+            self._plans[key] = plan
+        if plan.neg:
+            inputs = tuple(t.contiguous() if isinstance(t, torch.Tensor) else t for t in inputs)
+        M, N = plan.M, plan.N
+        a = _k_major_left(inputs[spec.left])
+        b = _k_major_right(inputs[spec.right])
         dev = a.device
-        operands = self._operand_tensors(inputs, M, N)
 
         tile = None
         if spec.store_tile:
-            tile = torch.empty_strided((M, N), (N, 1), dtype=spec.out_dtype, device=dev)
-        extras = [torch.empty_strided((M, N), (N, 1), dtype=dt, device=dev) for dt in spec.extra_dtypes]
+            tile = torch.empty((M, N), dtype=spec.out_dtype, device=dev)
+        extras = [torch.empty((M, N), dtype=dt, device=dev) for dt in spec.extra_dtypes]
         red_len = M if spec.reduce_axis == 1 else N
         reds = {name: torch.empty((red_len,), dtype=torch.float32, device=dev) for name in spec.reductions}
 
@@ -178,59 +245,39 @@ class HipKernelLauncher:
                     t.fill_(0.0 if name == "sum" else float("nan"))
             return self._assemble(tile, extras, reds)
 
-        key = (M, N, K, a.stride(0), b.stride(1), tuple((o.stride(), o.dtype) for o in operands))
-        d = self._desc(key)
-        d.M, d.N, d.K = M, N, K
+        d = plan.desc
         d.a, d.lda = a.data_ptr(), a.stride(0)
         d.b, d.ldb = b.data_ptr(), b.stride(1)
-        d.ab_dtype = _dtype_code(a.dtype)
-        d.n_ops = len(spec.ops)
-        if d.n_ops > _abi.MAX_OPS:
-            raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "too many epilogue ops")
-        for i, op in enumerate(spec.ops):
-            e = d.ops[i]
-            e.kind = _abi.OP_CODES[op.kind]
-            if op.kind in ("add", "mul"):
-                e.operand = self._operand_slot[op.operand]
-            else:
-                e.operand = op.operand
-            e.scalar = op.scalar
-        d.n_operands = len(operands)
-        if d.n_operands > _abi.MAX_OPERANDS:
-            raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "too many epilogue operands")
-        for i, t in enumerate(operands):
-            o = d.operands[i]
-            sm, sn = t.stride()
-            o.ptr = t.data_ptr()
-            o.stride_m, o.stride_n = sm, sn
-            o.extent = (M - 1) * sm + (N - 1) * sn + 1
-            o.dtype = _DTYPE_CODE[t.dtype]
-        if tile is not None:
-            d.out.ptr, d.out.ld, d.out.dtype = tile.data_ptr(), N, _dtype_code(tile.dtype)
-        else:
-            d.out.ptr, d.out.ld, d.out.dtype = None, N, _abi.BF16
-        d.n_extra = len(extras)
+        rebuilt = []  # operands built for this call, alive until the launch is queued
+        for i, (idx, rebuild) in enumerate(plan.operands):
+            t = inputs[idx]
+            if rebuild:
+                t = self._operand_tensor(t, idx, M, N)
+                rebuilt.append(t)
+            d.operands[i].ptr = t.data_ptr()
+        d.out.ptr = tile.data_ptr() if tile is not None else None
         for i, t in enumerate(extras):
-            d.extra[i].ptr, d.extra[i].ld, d.extra[i].dtype = t.data_ptr(), N, _dtype_code(t.dtype)
-        mask = 0
+            d.extra[i].ptr = t.data_ptr()
         for name, t in reds.items():
-            mask |= _abi.RED_BITS[name]
             d.reduce_out[_abi.RED_SLOT[name]] = t.data_ptr()
-        d.reduce_mask = mask
-        d.reduce_axis = spec.reduce_axis
 
         stream = torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0
         timing = self.timing_events
         if timing is not None:
-            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if self.timing_pool:
+                ev0, ev1 = self.timing_pool.pop()
+            else:
+                ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             ev0.record()
         rc = self._lib.fuseml_gemm_epilogue(ctypes.byref(d), ctypes.c_void_p(stream))
         if rc != _abi.OK:
             raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
         if timing is not None:
             ev1.record()
-            outs = [t for t in [tile, *extras, *reds.values()] if t is not None]
-            timing.append((ev0, ev1, (M, N, K), _distinct_bytes([*inputs, *outs])))
+            if plan.nbytes is None:
+                outs = [t for t in [tile, *extras, *reds.values()] if t is not None]
+                plan.nbytes = _distinct_bytes([inputs[i] for i in self._used] + outs)
+            timing.append((ev0, ev1, (M, N, plan.K), plan.nbytes))
         self.launch_count += 1
         return self._assemble(tile, extras, reds)
 
@@ -254,11 +301,6 @@ class HipKernelLauncher:
     def __call__(self, *inputs: torch.Tensor) -> Any:
         if len(inputs) != self._n_inputs:
             raise ValueError(f"Expected {self._n_inputs} input tensor(s), got {len(inputs)}.")
-        if any(_has_negative_stride(t) for t in inputs if isinstance(t, torch.Tensor)):
-            inputs = tuple(
-                t.contiguous() if isinstance(t, torch.Tensor) and _has_negative_stride(t) else t
-                for t in inputs
-            )
         if self._fallback_guard is not None:
             return self._fallback_guard.execute(lambda: self.launch(*inputs), inputs)
         return self.launch(*inputs)
