@@ -233,3 +233,60 @@ def test_empty_rows_give_empty_reductions():
                         reduce_axis=1, reduce_dtypes=(torch.float32,), outputs=(("tile",), ("red", "amax")))
     tile, mx = make(spec, 2, rec)(x, w.t())
     assert tile.shape == (0, 8) and mx.shape == (0,) and rec.calls == []
+
+
+def test_plan_reuse_takes_each_calls_pointers():
+    """The descriptor's non-pointer fields are filled once per input signature;
+    every call still sets its own input and output pointers."""
+    rec = Recorder()
+    spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("add", 3)), BF)
+    M, N, K = 16, 24, 32
+    launcher = make(spec, 4, rec)
+
+    def args():
+        return (torch.randn(N, dtype=BF), torch.randn(M, K, dtype=BF), torch.randn(N, K, dtype=BF).t(),
+                torch.randn(M, N, dtype=BF))
+
+    first, second = args(), args()
+    out1 = launcher(*first)
+    out2 = launcher(*second)
+    assert len(launcher._plans) == 1
+    c1, c2 = rec.calls
+    assert (c1["a"], c1["b"]) == (first[1].data_ptr(), first[2].data_ptr())
+    assert (c2["a"], c2["b"]) == (second[1].data_ptr(), second[2].data_ptr())
+    assert c1["operands"] == c2["operands"] == [(0, 1, N, _abi.BF16), (N, 1, M * N, _abi.BF16)]
+    assert out1 is not out2 and out1.shape == out2.shape == (M, N)  # fresh outputs per call
+
+
+def test_plan_rebuilds_converted_operands_every_call():
+    """An operand the kernel cannot read in its own dtype (int here) is converted
+    per call, and the descriptor points at that call's converted copy."""
+    seen = []
+
+    class PtrRecorder(Recorder):
+        def fuseml_gemm_epilogue(self, desc_ref, stream):
+            d = ctypes.cast(desc_ref, ctypes.POINTER(_abi.GemmDesc)).contents
+            seen.append((d.operands[0].ptr, d.operands[0].dtype))
+            return super().fuseml_gemm_epilogue(desc_ref, stream)
+
+    rec = PtrRecorder()
+    spec = EpilogueSpec(1, 2, (EpiOp("add", 0),), BF)
+    M, N, K = 8, 16, 24
+    launcher = make(spec, 3, rec)
+    x, wt = torch.randn(M, K, dtype=BF), torch.randn(N, K, dtype=BF).t()
+    b1, b2 = torch.arange(N, dtype=torch.int32), torch.arange(N, dtype=torch.int32) * 2
+    launcher(b1, x, wt)
+    launcher(b2, x, wt)
+    assert len(launcher._plans) == 1
+    assert [dt for _, dt in seen] == [_abi.F32, _abi.F32]
+    assert seen[0][0] not in (b1.data_ptr(), b2.data_ptr()) and seen[1][0] not in (b1.data_ptr(), b2.data_ptr())
+
+
+def test_new_signature_gets_its_own_plan():
+    rec = Recorder()
+    spec = EpilogueSpec(0, 1, (EpiOp("relu"),), BF)
+    launcher = make(spec, 2, rec)
+    launcher(torch.randn(8, 16, dtype=BF), torch.randn(24, 16, dtype=BF).t())
+    launcher(torch.randn(40, 16, dtype=BF), torch.randn(24, 16, dtype=BF).t())
+    assert len(launcher._plans) == 2
+    assert [(c["M"], c["N"], c["K"]) for c in rec.calls] == [(8, 24, 16), (40, 24, 16)]
