@@ -1280,8 +1280,8 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       A[j][(int)r] = (expr);                        \
     });                                                  \
   })
-          case FUSEML_OP_RELU:  // NaN passes through, as in torch.relu
-            FUSEML_EACH(v < 0.0f ? 0.0f : v);
+          case FUSEML_OP_RELU:  // one v_maximum3_f32; NaN passes through, as in torch.relu
+            FUSEML_EACH(max_nan(v, 0.0f));
             break;
 #define FUSEML_EACH_N(fn)                                \
   static_for<0, NJ>([&](auto j) {                        \
