@@ -144,6 +144,43 @@ def test_c4_default_discovery_matches_reference_grouping():
     _close(h, _f64(rh), "C4 tile vs eager")
 
 
+def test_compiled_c4_replays_in_a_hip_graph():
+    """The compiled module (fused GEMM + ReLU + three row reductions) captured
+    in a HIP graph: every replay, after a new input is copied in and with an
+    eager call of the compiled module between replays, matches that eager
+    call (tile and amax bit for bit, sum and mean to 1e-5 relative)."""
+    from fuseml_amd.workloads import c4_gemm_row_reductions
+
+    wl = c4_gemm_row_reductions(scale=1 / 8).to("cuda")  # x[1024,2048] -> [1024,8192]
+    compiled, be = _compile(wl.model, fuse_sibling_reductions=True)
+    x = wl.inputs[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.no_grad(), torch.cuda.stream(side):
+        compiled(x)  # compile and build the launch plan outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph):
+        outs = compiled(x)
+    assert be.fusion_applied and len(be.launchers) == 1
+    gen = torch.Generator().manual_seed(9)
+    for i in range(3):
+        x.copy_(torch.randn(x.shape, generator=gen).to(x.dtype))
+        with torch.no_grad():
+            eager = compiled(x)
+        torch.cuda.synchronize()
+        for o in outs:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, g, e in zip(("tile", "sum", "amax", "mean"), outs, eager):
+            if name in ("tile", "amax"):
+                assert torch.equal(g, e), f"replay {i}: {name} differs from the eager call"
+            else:
+                assert torch.allclose(g, e, rtol=1e-5, atol=1e-5), f"replay {i}: {name}"
+
+
 def test_c5_stacked_compiled_two_blocks():
     from fuseml_amd.workloads import c5_stacked_mlp
 

@@ -440,6 +440,57 @@ def test_transposed_and_strided_gemm_operands():
     _check_tile(out, ref, "relayout")
 
 
+@pytest.mark.parametrize("forced_variant", ["auto", "large", "deep3"], indirect=True)
+def test_graph_capture_replays(forced_variant):
+    """A fused launch captured in a HIP graph (torch.cuda.CUDAGraph).  The
+    launcher only queues work on the current stream: the reduction buffers are
+    cleared by a fill kernel, not a memset, and nothing is read back to the
+    host.  Each replay, after new values are copied into the captured inputs
+    and with eager launches and synchronisations between replays, gives the
+    eager launch's tile and amax bit for bit, and the oracle's sum."""
+    M, N, K = 600, 1030, 192
+    dtype = torch.bfloat16
+    steps = [("add", 0, 1.0), ("gelu_erf", -1, 1.0), ("add", 1, 1.0)]
+    spec = _spec(left=2, right=3, ops=steps, out_dtype=dtype, store_tile=True,
+                 reductions=("sum", "amax"), reduce_axis=1,
+                 reduce_dtypes=(torch.float32, torch.float32),
+                 outputs=(("tile",), ("red", "sum"), ("red", "amax")))
+    L = _launcher(spec, 4)
+
+    def host_inputs(seed):
+        a, w = _gemm_inputs(M, N, K, dtype, seed=seed)
+        bias = (torch.rand(N, generator=_gen(seed + 2)) - 0.5).to(dtype)
+        resid = torch.randn(M, N, generator=_gen(seed + 3)).to(dtype)
+        return [bias, resid, a, w.t()]
+
+    print(f"case graph capture variant={forced_variant}", flush=True)
+    static = [t.cuda() for t in host_inputs(40)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        L(*static)  # first call builds the launch plan outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g_tile, g_sum, g_amax = L(*static)
+    for seed in (41, 42, 43):
+        host = host_inputs(seed)
+        for dst, src in zip(static, host):
+            dst.copy_(src)
+        e_tile, _, e_amax = L(*static)  # eager launch on the same inputs
+        torch.cuda.synchronize()
+        g_tile.fill_(float("nan"))  # a replay that wrote nothing would show
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_tile, e_tile), f"replay seed {seed}: tile differs from eager"
+        assert torch.equal(g_amax, e_amax), f"replay seed {seed}: amax differs from eager"
+        ref = ora.gemm_epilogue([_np(t) for t in host], 2, 3, steps, ("sum", "amax"), 1)
+        _check_tile(g_tile, ref["tile"], f"replay seed {seed}")
+        _check_red(g_sum, ref["sum"], np.abs(ref["tile"]).sum(axis=1), f"replay seed {seed} sum")
+        _check_red(g_amax, ref["amax"], np.abs(ref["tile"]).max(axis=1), f"replay seed {seed} amax")
+
+
 # ---------------------------------------------------------------------------
 # Full-size configurations, checked at sampled rows
 # ---------------------------------------------------------------------------
