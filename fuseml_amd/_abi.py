@@ -17,7 +17,7 @@ import os
 import threading
 from typing import Optional
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_OPS = 16
 MAX_OPERANDS = 8
 MAX_EXTRA_OUT = 4
@@ -76,6 +76,7 @@ EXPORTED_SYMBOLS = (
     "fuseml_mfma_peak_probe",
     "fuseml_mlp_block",
     "fuseml_mlp_block_supported",
+    "fuseml_split_bf16x3",
 )
 
 
@@ -198,6 +199,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fuseml_desc_size.restype = ctypes.c_size_t
     lib.fuseml_mlp_desc_size.argtypes = []
     lib.fuseml_mlp_desc_size.restype = ctypes.c_size_t
+    i64 = ctypes.c_int64
+    lib.fuseml_split_bf16x3.argtypes = [ctypes.c_void_p, i64, i64, i64, i64, ctypes.c_void_p, i64, i64,
+                                        ctypes.c_uint32, ctypes.c_void_p]
+    lib.fuseml_split_bf16x3.restype = ctypes.c_int
 
 
 def check_abi(lib: ctypes.CDLL) -> None:
@@ -225,8 +230,8 @@ def load_library() -> ctypes.CDLL:
                 "(or __graft_entry__.build()) first"
             )
         lib = ctypes.CDLL(path)
+        check_abi(lib)  # before binding: an older library lacks newer entry points
         _declare(lib)
-        check_abi(lib)
         _lib = lib
         return lib
 

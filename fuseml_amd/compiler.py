@@ -22,7 +22,8 @@ attributes ``fusion_applied`` / ``fusion_strategy`` / ``fusion_candidates``):
 
 The cost model (replacing topology.py:479-571's NVIDIA tables and the
 Triton/cuBLAS/bypass split) is two-way: the fused HIP kernel when the device
-is gfx950, the operands are bf16/f16, the group fits one launch and its output
+is gfx950, the operands are bf16/f16 (or fp32, run as a three-term bf16 split
+product), the group fits one launch and its output
 has at least ``min_output_elements`` (the reference's tiny-output rule,
 fusion_pass.py:463 and 498: M*N < 500 000 bypasses), the GEMM is not a
 few-tile problem with a long K loop, and the epilogue saves more than the K
@@ -57,7 +58,14 @@ MIN_TILES_LONG_K = 256  # 128x128 output tiles; MI355X has 256 CUs
 # Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the
 # eager path would run over the [M,N] output): measured crossover on MI355X.
 K_PER_EPILOGUE_PASS = 1024
-SUPPORTED_GEMM_DTYPES = (torch.bfloat16, torch.float16)
+# fp32 operands run as a three-term bf16 split product (K' = 3 ceil8(K)).
+SUPPORTED_GEMM_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def effective_k(K: int, dtype: Any) -> int:
+    """Length of the K loop the kernel runs: 3 ceil8(K) for fp32 operands (the
+    split product), K otherwise."""
+    return 3 * (-(-K // 8) * 8) if dtype == torch.float32 else K
 
 
 class _NoFusionPossible(Exception):
@@ -85,18 +93,19 @@ def device_is_gfx950(device: Optional[torch.device] = None) -> bool:
     return str(arch).startswith("gfx950")
 
 
-def _gemm_k(group: Any) -> Optional[int]:
-    """K of the group's GEMM from the left operand's metadata (None if unknown)."""
+def _gemm_k(group: Any) -> Tuple[Optional[int], Any]:
+    """(K, dtype) of the group's GEMM from the left operand's metadata (K None
+    if unknown)."""
     base = group.base_node
     args = (getattr(group, "node_args_snapshot", None) or {}).get(base.name, base.args)
     mat1 = args[1] if base.target is TRIGGER_TARGETS[0] else args[0]
     m = _meta(mat1)
     if m is None or len(m.shape) != 2:
-        return None
+        return None, None
     try:
-        return int(m.shape[1])
+        return int(m.shape[1]), getattr(m, "dtype", None)
     except (TypeError, ValueError):
-        return None
+        return None, None
 
 
 def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
@@ -112,16 +121,18 @@ def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSIO
     if len(m1.shape) != 2 or len(m2.shape) != 2:
         return False, "GEMM operands are not 2-D"
     if m1.dtype not in SUPPORTED_GEMM_DTYPES or m2.dtype != m1.dtype:
-        return False, f"GEMM dtype {m1.dtype}: no MFMA variant (bf16/f16 only)"
+        return False, f"GEMM dtype {m1.dtype}/{m2.dtype}: no MFMA variant (bf16, f16, fp32 split)"
     M, K = int(m1.shape[0]), int(m1.shape[1])
     N = int(m2.shape[1])
     if M * N < min_output_elements:
         return False, f"tiny output {M}x{N}"
-    if K % 8 != 0:
+    if K % 8 != 0 and m1.dtype != torch.float32:  # the fp32 split pads K
         return False, f"K={K} is not a multiple of 8"
     tiles = -(-M // 128) * -(-N // 128)
-    if K >= LONG_K and tiles < min_tiles_long_k:
-        return False, f"{tiles} output tiles at K={K}: fewer tiles than CUs with a long K loop"
+    k_loop = effective_k(K, m1.dtype)
+    if k_loop >= LONG_K and tiles < min_tiles_long_k:
+        k_txt = f"K={K}" if k_loop == K else f"K={K} (a K loop of {k_loop})"
+        return False, f"{tiles} output tiles at {k_txt}: fewer tiles than CUs with a long K loop"
     return True, "fused"
 
 
@@ -176,7 +187,8 @@ def epilogue_passes(spec: EpilogueSpec) -> int:
     return passes + len(spec.reductions)
 
 
-def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOGUE_PASS) -> Tuple[bool, str]:
+def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOGUE_PASS,
+                      dtype: Any = None) -> Tuple[bool, str]:
     """The fused kernel against eager (hipBLASLt GEMM + elementwise kernels).
 
     Measured on one MI355X, each fused group against its eager ops (same box,
@@ -189,8 +201,11 @@ def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOG
     against 0.829 ms) and K = 16384 (bias + residual: 0.801 against 0.714 ms);
     with four passes it wins at K = 1024 (C3: 0.201 against 0.313 ms) and
     K = 2048 (ReLU + three row reductions: 0.269 against 0.374 ms).  Rule: fuse
-    iff K <= k_per_pass * passes; k_per_pass = 0 always fuses."""
-    if k_per_pass <= 0:
+    iff K <= k_per_pass * passes; k_per_pass = 0 always fuses.
+
+    fp32 groups always fuse: eager runs an fp32 GEMM at the fp32 MFMA rate
+    (157 TFLOP/s peak), the split product at a third of the bf16 rate."""
+    if k_per_pass <= 0 or dtype == torch.float32:
         return True, "fused"
     passes = epilogue_passes(spec)
     if K <= k_per_pass * passes:
@@ -324,8 +339,9 @@ class FuseMLCompiler:
                     logger.info("group %s stays eager: %s", group, exc)
                     spec = None
                 if spec is not None:
-                    K = _gemm_k(group)
-                    win, why = fused_beats_eager(spec, K, self.k_per_epilogue_pass) if K else (True, "fused")
+                    K, ab_dtype = _gemm_k(group)
+                    win, why = (fused_beats_eager(spec, K, self.k_per_epilogue_pass, ab_dtype)
+                                if K else (True, "fused"))
                     if not win:
                         logger.info("group %s stays eager: %s", group, why)
                         spec = None

@@ -52,6 +52,7 @@
 #include <type_traits>
 
 #include "fuseml_hip.h"
+#include "gelu_phi.h"
 
 namespace {
 
@@ -263,23 +264,10 @@ __device__ __forceinline__ void atomic_max_f32(float* p, float v) {
 }
 
 
-// Standard normal CDF for GELU (approximate='none'):
-//   Phi(x) = 0.5 (1 + erf(x / sqrt 2)) ~= 0.5 + x * Q(x^2)  for |x| <= 3 sqrt 2,
-// with x clamped to that range beyond it (Phi(3 sqrt 2) = 1 - 1.1e-5).  Q is
-// the least-squares fit of erf(z)/z in z^2 on [0, 3] (fuseml_amd/csrc/fit_erf.py,
-// |erf error| <= 3.3e-5) with the 1/sqrt 2 and 1/2 scalings folded into its
-// coefficients: Q_k = P_k / (2 sqrt 2 * 2^k); |Phi error| <= 3.3e-5 in float32.
-// Only FMAs: GELU costs 12 VALU ops and no quarter-rate transcendentals.
-constexpr float kPhiClamp = 4.2426406871192851f;  // 3 sqrt 2
-constexpr float kPhiQ0 = 3.989064909e-01f;
-constexpr float kPhiQ1 = -6.635807263e-02f;
-constexpr float kPhiQ2 = 9.828446245e-03f;
-constexpr float kPhiQ3 = -1.113571280e-03f;
-constexpr float kPhiQ4 = 9.446521791e-05f;
-constexpr float kPhiQ5 = -5.748589919e-06f;
-constexpr float kPhiQ6 = 2.335694047e-07f;
-constexpr float kPhiQ7 = -5.604949355e-09f;
-constexpr float kPhiQ8 = 5.955950179e-11f;
+// Standard normal CDF for GELU (approximate='none'): the constrained fit of
+// gelu_phi.h (|Phi error| <= 1.5e-5 in float32; beyond the clamp Phi is 1
+// above and 2e-8 below, so GELU there is x or ~0).
+using namespace fuseml_phi;
 
 // LDS stage geometry for a K depth of BK 16-bit elements.  A stage row (one row
 // of A or of W) is BK*2 bytes = BK/8 chunks of 16 bytes.  A ds_read_b128 is

@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "fuseml_hip.h"
+#include "gelu_phi.h"
 
 namespace fuseml_detail {
 // The library's error text (fuseml_last_error), shared with gemm_epilogue.hip.
@@ -114,20 +115,20 @@ __device__ __forceinline__ uint32_t pack2<_Float16>(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
 }
 
-// GELU(erf): x * Phi(x), Phi(x) = 0.5 + xc * Q(xc^2), xc = clamp(x, +-3 sqrt 2);
-// Q is the least-squares fit of erf(z)/z of fuseml_amd/csrc/fit_erf.py (the
-// same coefficients as the GEMM+epilogue kernels; |Phi error| <= 3.3e-5).
+// GELU(erf): x * Phi(x), Phi(x) = 0.5 + xc * Q(xc^2), xc = clamp(x, +-3 sqrt 2),
+// with the constants of gelu_phi.h (the same as the GEMM+epilogue kernels').
 __device__ __forceinline__ float gelu_erf(float x) {
-  const float xc = __builtin_amdgcn_fmed3f(x, -4.2426406871192851f, 4.2426406871192851f);
+  using namespace fuseml_phi;
+  const float xc = __builtin_amdgcn_fmed3f(x, -kPhiClamp, kPhiClamp);
   const float t = xc * xc;
-  float q = fmaf(5.955950179e-11f, t, -5.604949355e-09f);
-  q = fmaf(q, t, 2.335694047e-07f);
-  q = fmaf(q, t, -5.748589919e-06f);
-  q = fmaf(q, t, 9.446521791e-05f);
-  q = fmaf(q, t, -1.113571280e-03f);
-  q = fmaf(q, t, 9.828446245e-03f);
-  q = fmaf(q, t, -6.635807263e-02f);
-  q = fmaf(q, t, 3.989064909e-01f);
+  float q = fmaf(kPhiQ8, t, kPhiQ7);
+  q = fmaf(q, t, kPhiQ6);
+  q = fmaf(q, t, kPhiQ5);
+  q = fmaf(q, t, kPhiQ4);
+  q = fmaf(q, t, kPhiQ3);
+  q = fmaf(q, t, kPhiQ2);
+  q = fmaf(q, t, kPhiQ1);
+  q = fmaf(q, t, kPhiQ0);
   return x * fmaf(xc, q, 0.5f);
 }
 

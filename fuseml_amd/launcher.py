@@ -82,12 +82,15 @@ class _Plan:
     and for each operand slot the input it comes from and whether it must be
     rebuilt per call (a dtype conversion or a broadcast that merging copies)."""
 
-    __slots__ = ("desc", "M", "N", "K", "neg", "operands", "nbytes")
+    __slots__ = ("desc", "M", "N", "K", "neg", "operands", "nbytes", "k_split")
 
     def __init__(self) -> None:
         self.desc = _abi.GemmDesc()
         self.M = self.N = self.K = 0
         self.neg = False
+        # fp32 GEMM operands: the bf16 segment width k_pad of the three-term
+        # split (the kernel then runs K' = 3 k_pad); 0 for bf16/f16 operands.
+        self.k_split = 0
         self.operands: List[Tuple[int, bool]] = []  # (input index, rebuilt per call)
         self.nbytes: Optional[int] = None  # algorithmic bytes, for the timing hook
 
@@ -163,18 +166,23 @@ class HipKernelLauncher:
         plan.neg = any(_has_negative_stride(inputs[i]) for i in self._used if isinstance(inputs[i], torch.Tensor))
         if plan.neg:
             inputs = tuple(t.contiguous() if isinstance(t, torch.Tensor) else t for t in inputs)
-        a = _k_major_left(inputs[spec.left])
-        b = _k_major_right(inputs[spec.right])
-        if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
+        a, b = inputs[spec.left], inputs[spec.right]
+        if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16, torch.float32):
             raise _abi.FuseMLHipError(
-                _abi.EUNSUPPORTED, f"GEMM operands {a.dtype}/{b.dtype}: bf16/f16 MFMA only"
+                _abi.EUNSUPPORTED, f"GEMM operands {a.dtype}/{b.dtype}: bf16, f16 or fp32 (split) only"
             )
         M, K = int(a.shape[0]), int(a.shape[1])
         N = int(b.shape[1])
         plan.M, plan.N, plan.K = M, N, K
         d = plan.desc
         d.M, d.N, d.K = M, N, K
-        d.ab_dtype = _dtype_code(a.dtype)
+        if a.dtype == torch.float32:
+            # One bf16 GEMM over [hi|hi|lo] . [hi|lo|hi]: K' = 3 k_pad.
+            plan.k_split = -(-K // 8) * 8
+            d.K = 3 * plan.k_split
+            d.ab_dtype = _abi.BF16
+        else:
+            d.ab_dtype = _dtype_code(a.dtype)
         order = self._operand_order()
         slot = {idx: i for i, idx in enumerate(order)}
         d.n_ops = len(spec.ops)
@@ -223,8 +231,9 @@ class HipKernelLauncher:
         if plan.neg:
             inputs = tuple(t.contiguous() if isinstance(t, torch.Tensor) else t for t in inputs)
         M, N = plan.M, plan.N
-        a = _k_major_left(inputs[spec.left])
-        b = _k_major_right(inputs[spec.right])
+        a, b = inputs[spec.left], inputs[spec.right]
+        if not plan.k_split:
+            a, b = _k_major_left(a), _k_major_right(b)
         dev = a.device
 
         tile = None
@@ -246,8 +255,14 @@ class HipKernelLauncher:
             return self._assemble(tile, extras, reds)
 
         d = plan.desc
-        d.a, d.lda = a.data_ptr(), a.stride(0)
-        d.b, d.ldb = b.data_ptr(), b.stride(1)
+        stream = torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0
+        if plan.k_split:
+            a, b = self._split_operands(plan, a, b, stream)
+            d.a, d.lda = a.data_ptr(), a.stride(0)
+            d.b, d.ldb = b.data_ptr(), b.stride(0)
+        else:
+            d.a, d.lda = a.data_ptr(), a.stride(0)
+            d.b, d.ldb = b.data_ptr(), b.stride(1)
         rebuilt = []  # operands built for this call, alive until the launch is queued
         for i, (idx, rebuild) in enumerate(plan.operands):
             t = inputs[idx]
@@ -261,7 +276,6 @@ class HipKernelLauncher:
         for name, t in reds.items():
             d.reduce_out[_abi.RED_SLOT[name]] = t.data_ptr()
 
-        stream = torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0
         timing = self.timing_events
         if timing is not None:
             if self.timing_pool:
@@ -280,6 +294,26 @@ class HipKernelLauncher:
             timing.append((ev0, ev1, (M, N, plan.K), plan.nbytes))
         self.launch_count += 1
         return self._assemble(tile, extras, reds)
+
+    def _split_operands(self, plan: _Plan, a: torch.Tensor, b: torch.Tensor, stream: int):
+        """fp32 GEMM operands as bf16 split parts on the launch stream:
+        A3 [M, 3 k_pad] = [hi|hi|lo] of A, B3 [N, 3 k_pad] = [hi|lo|hi] of the
+        weight rows (B[k, n] = b[k, n]), so that A3 . B3^T is the three-term
+        product.  Both are rebuilt on every call (4 bytes read and 6 written
+        per element of each operand); caching B3 for a weight would need a
+        reliable signal that the weight is unchanged."""
+        kp = plan.k_split
+        M, N, K = plan.M, plan.N, plan.K
+        a3 = torch.empty((M, 3 * kp), dtype=torch.bfloat16, device=a.device)
+        b3 = torch.empty((N, 3 * kp), dtype=torch.bfloat16, device=b.device)
+        for src, rows, sr, sk, dst, mask in ((a, M, a.stride(0), a.stride(1), a3, 0b100),
+                                             (b, N, b.stride(1), b.stride(0), b3, 0b010)):
+            rc = self._lib.fuseml_split_bf16x3(ctypes.c_void_p(src.data_ptr()), rows, K, sr, sk,
+                                               ctypes.c_void_p(dst.data_ptr()), 3 * kp, kp, mask,
+                                               ctypes.c_void_p(stream))
+            if rc != _abi.OK:
+                raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
+        return a3, b3
 
     def _assemble(self, tile, extras, reds) -> Any:
         outs = []

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FUSEML_ABI_VERSION 2
+#define FUSEML_ABI_VERSION 3
 
 #define FUSEML_MAX_OPS 16
 #define FUSEML_MAX_OPERANDS 8
@@ -213,6 +213,25 @@ int fuseml_mlp_block(const fuseml_mlp_desc* desc, void* stream);
 
 /* 1 if fuseml_mlp_block accepts `desc`, 0 if not (reason in fuseml_last_error()). */
 int fuseml_mlp_block_supported(const fuseml_mlp_desc* desc);
+
+/* ------------------------------------------------------------------------
+ * fp32 GEMM operands.  Writes the bf16 parts of an fp32 matrix so that the
+ * fused kernel can run an fp32 group as one bf16 GEMM over a K axis three
+ * times as long (a three-term split product, about 16 mantissa bits per
+ * input).  Replaces Triton's default tf32 `tl.dot` on fp32 inputs
+ * (fuseml/codegen/kernel_generator.py:1536), which keeps 10.
+ *
+ * src element (r,k) is src[r*stride_r + k*stride_k], r < rows, k < K (any
+ * non-negative strides).  Row r of dst (bf16, row stride ld_dst) is three
+ * segments of k_pad columns; segment s holds lo(x) = bf16(x - bf16(x)) if
+ * bit s of lo_mask is set, else hi(x) = bf16(x); columns K..k_pad-1 are 0.
+ * With A3 from lo_mask 4 (hi|hi|lo) and B3 from lo_mask 2 (hi|lo|hi),
+ * A3 . B3 = hi.hi + hi.lo + lo.hi.  Needs k_pad % 8 == 0, k_pad >= K,
+ * ld_dst % 8 == 0, ld_dst >= 3 k_pad and a 16-byte aligned dst.
+ * Asynchronous on `stream`; 0 or a FUSEML_E* code.
+ * ------------------------------------------------------------------------ */
+int fuseml_split_bf16x3(const float* src, int64_t rows, int64_t K, int64_t stride_r, int64_t stride_k, void* dst,
+                        int64_t ld_dst, int64_t k_pad, uint32_t lo_mask, void* stream);
 
 /* Measurement only (no reference counterpart; the reference's benchmark
  * prices against a spec table, benchmarks/bench_mlp_block.py:228-412): launch

@@ -99,12 +99,36 @@ def test_tiny_output_bypasses(recorded):
     assert be.fusion_applied is False and recorded.built == []
 
 
-def test_fp32_gemm_bypasses(recorded):
-    m = TransformerMLP(64, 256).eval()
+def test_fp32_gemm_fuses_as_split_product(recorded):
+    """fp32 groups fuse (the reference fuses them through Triton's tf32 dot,
+    kernel_generator.py:1536); K need not be a multiple of 8 (the split pads
+    it), and the K-per-pass crossover, calibrated against eager bf16 GEMMs,
+    does not apply (eager fp32 runs at the fp32 MFMA rate)."""
+    m = TransformerMLP(60, 256).eval()
     be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
     with torch.no_grad():
-        _compile(m, be)(torch.randn(32, 64))
+        out = _compile(m, be)(torch.randn(32, 60))
+        ref = m(torch.randn(32, 60))
+    assert out.dtype == torch.float32 and out.shape == ref.shape
+    assert be.fusion_applied and [s.spec.describe() for s in recorded.built] == [
+        "gemm(1,2) -> add[0] -> gelu_erf", "gemm(1,2) -> add[0] -> add[3]"]
+    assert comp.fused_beats_eager(recorded.built[1].spec, 16384, dtype=torch.float32)[0]
+    assert not comp.fused_beats_eager(recorded.built[1].spec, 16384, dtype=torch.bfloat16)[0]
+
+
+def test_fp64_gemm_bypasses(recorded):
+    m = TransformerMLP(64, 256).to(torch.float64).eval()
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        _compile(m, be)(torch.randn(32, 64, dtype=torch.float64))
     assert be.fusion_applied is False and recorded.built == []
+
+
+def test_fp32_few_tiles_rule_uses_the_split_k_loop():
+    """The few-tile rule looks at the K loop the kernel runs: 3 ceil8(K) for fp32."""
+    assert comp.effective_k(1000, torch.float32) == 3000
+    assert comp.effective_k(1001, torch.float32) == 3024
+    assert comp.effective_k(1000, torch.bfloat16) == 1000
 
 
 def test_unbuildable_group_runs_eager(monkeypatch):

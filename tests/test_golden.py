@@ -4,7 +4,8 @@ CPU tier: the oracle reproduces every fixture.
 GPU tier: the HIP kernel family (one fused launch per group, through the C ABI)
 reproduces the bf16 fixtures within the stated tolerances
 (tiles rtol/atol 2e-2; fp32 reductions 1e-2 of |ref|, floored at 1e-3 of the
-reduction of |v|).
+reduction of |v|), and the fp32 fixture through the fp32 split path to
+rtol/atol 1e-4.
 """
 
 import os
@@ -155,3 +156,25 @@ def test_hip_stacked_golden():
         y = _launch([("add", 0), ("add", 3)], 1, 2, 4, _t(d[f"b2_{i}"]), h, _t(d[f"w2_{i}"]).t(), y)
     torch.cuda.synchronize()
     _close(y, d["y"], "y")
+
+
+@pytest.mark.gpu
+def test_hip_transformer_mlp_tanh_fp32_golden():
+    """The fp32 fixture through the fp32 path (both GEMM operands split into
+    bf16 parts, fp32 epilogue and output): torch eager fp32's values to 1e-4."""
+    from fuseml_amd.epilogue import EpilogueSpec, EpiOp
+    from fuseml_amd.launcher import HipKernelLauncher
+
+    d = load("transformer_mlp_tanh_fp32")
+    f32 = torch.float32
+
+    def launch(ops, *args):
+        spec = EpilogueSpec(left=1, right=2, ops=tuple(EpiOp(*o) for o in ops), out_dtype=f32)
+        return HipKernelLauncher(spec, len(args))(*args)
+
+    h = launch([("add", 0), ("gelu_tanh",)], _t(d["b1"], f32), _t(d["x"], f32), _t(d["w1"], f32).t())
+    y = launch([("add", 0)], _t(d["b2"], f32), h, _t(d["w2"], f32).t())
+    torch.cuda.synchronize()
+    assert h.dtype == y.dtype == f32
+    g = y.cpu().numpy().astype(np.float64)
+    assert np.allclose(g, d["y"], rtol=1e-4, atol=1e-4), f"max err {np.abs(g - d['y']).max()}"

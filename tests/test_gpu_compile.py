@@ -181,6 +181,29 @@ def test_compiled_c4_replays_in_a_hip_graph():
                 assert torch.allclose(g, e, rtol=1e-5, atol=1e-5), f"replay {i}: {name}"
 
 
+def test_fp32_mlp_compiled_as_split_products():
+    """An fp32 TransformerMLP (x[2048,1024] -> 4096 -> 1024): both groups fuse,
+    each GEMM as one bf16 launch over the split operands; the result matches
+    the float64 oracle to 1e-4 (eager fp32 is also within that)."""
+    from fuseml_amd.workloads import TransformerMLP
+
+    torch.manual_seed(5)
+    m = TransformerMLP(1024, 4096).eval().to("cuda")
+    x = torch.randn(2048, 1024, generator=torch.Generator().manual_seed(6)).to("cuda")
+    compiled, be = _compile(m)
+    with torch.no_grad():
+        y = compiled(x)
+        eager = m(x)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and len(be.launchers) == 2 and _launches(be) == 2
+    assert y.dtype == torch.float32
+    ref = ora_w.transformer_mlp(_f64(x), _f64(m.linear1.weight), _f64(m.linear1.bias),
+                                _f64(m.linear2.weight), _f64(m.linear2.bias))
+    for got, what in ((y, "fused fp32"), (eager, "eager fp32")):
+        g = _f64(got)
+        assert np.allclose(g, ref, rtol=1e-4, atol=1e-4), f"{what}: max err {np.abs(g - ref).max()}"
+
+
 def test_c5_stacked_compiled_two_blocks():
     from fuseml_amd.workloads import c5_stacked_mlp
 

@@ -11,7 +11,9 @@ Tolerances (stated by the benchmark contract):
   * fp32 reductions: ``|red - ref| <= 1e-2 * |ref|``, floored at
     ``1e-2 * 1e-3 * ref_abs`` where ``ref_abs`` is the same reduction of
     ``|v|`` (only a sum or mean that cancels to within 0.1% of its scale
-    reaches the floor).
+    reaches the floor);
+  * fp32 groups (GEMM operands split into bf16 parts): fp32 tiles and
+    reductions to rtol = atol = 1e-4; the split itself bit for bit.
 """
 
 from __future__ import annotations
@@ -489,6 +491,122 @@ def test_graph_capture_replays(forced_variant):
         _check_tile(g_tile, ref["tile"], f"replay seed {seed}")
         _check_red(g_sum, ref["sum"], np.abs(ref["tile"]).sum(axis=1), f"replay seed {seed} sum")
         _check_red(g_amax, ref["amax"], np.abs(ref["tile"]).max(axis=1), f"replay seed {seed} amax")
+
+
+# ---------------------------------------------------------------------------
+# fp32 GEMM groups: both operands split into bf16 parts (fuseml_split_bf16x3),
+# one bf16 GEMM over K' = 3 ceil8(K).  The split is integer/bit work and is
+# checked bit for bit; the fused fp32 results are checked against the float64
+# oracle to rtol = atol = 1e-4 (the reference's tf32 path is ~1e-3 off).
+# ---------------------------------------------------------------------------
+
+FP32_RTOL = 1e-4
+FP32_ATOL = 1e-4
+BF16_MAX = 3.38953139e38
+
+
+def _split_bits_ref(x: torch.Tensor):
+    """hi and lo bits of the split, from torch's own bf16 rounding: hi =
+    bf16(x) (RNE), or the truncated bits where that would overflow a finite x;
+    lo = bf16(x - hi) for finite x, else 0."""
+    fin = torch.isfinite(x)
+    big = fin & (x.abs() > BF16_MAX)
+    hi = torch.where(big, (x.view(torch.int32) >> 16).to(torch.int16), x.to(torch.bfloat16).view(torch.int16))
+    hi_f = (hi.to(torch.int32) << 16).view(torch.float32)
+    lo = torch.where(fin, x - hi_f, torch.zeros_like(x)).to(torch.bfloat16).view(torch.int16)
+    return hi, lo
+
+
+def _split_on_device(x: torch.Tensor, lo_mask: int):
+    from fuseml_amd import _abi
+
+    lib = _abi.load_library()
+    rows, K = x.shape
+    kp = -(-K // 8) * 8
+    dst = torch.full((rows, 3 * kp), 0x7777, dtype=torch.int16, device=x.device)
+    rc = lib.fuseml_split_bf16x3(x.data_ptr(), rows, K, x.stride(0), x.stride(1), dst.data_ptr(), 3 * kp, kp,
+                                 lo_mask, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _abi.last_error(lib)
+    torch.cuda.synchronize()
+    return dst.cpu(), kp
+
+
+@pytest.mark.parametrize("layout", ["contig", "ragged_k", "strided_k", "transposed", "one_row"])
+@pytest.mark.parametrize("lo_mask", [0b100, 0b010])
+def test_split_bf16x3_bit_exact(layout, lo_mask):
+    g = _gen(60)
+    shapes = {"contig": (300, 64), "ragged_k": (37, 100), "strided_k": (41, 3 * 77), "transposed": (56, 33),
+              "one_row": (1, 24)}
+    base = torch.randn(*shapes[layout], generator=g)
+    base = base * torch.exp2(torch.randint(-40, 40, base.shape, generator=g).float())
+    specials = [float("inf"), -float("inf"), float("nan"), -0.0, 1e-40, -3e-39, 3.3e38, -3.39e38,
+                3.4028235e38, 3.3895314e38, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -9]
+    base.view(-1)[: len(specials)] = torch.tensor(specials)
+    x = {"strided_k": lambda t: t[:, ::3], "transposed": lambda t: t.t()}.get(layout, lambda t: t)(base)
+    print(f"case split layout={layout} mask={lo_mask} shape={tuple(x.shape)} stride={x.stride()}", flush=True)
+    got, kp = _split_on_device(x.cuda(), lo_mask)
+    hi, lo = _split_bits_ref(x)
+    K = x.shape[1]
+    nan = torch.isnan(x)
+    for seg in range(3):
+        part = got[:, seg * kp: seg * kp + K]
+        if (lo_mask >> seg) & 1:
+            ok = part == lo                                   # lo of inf/NaN is 0
+        else:
+            as_f = (part.to(torch.int32) << 16).view(torch.float32)
+            ok = torch.where(nan, torch.isnan(as_f), part == hi)
+        assert ok.all(), f"segment {seg}: {(~ok).sum()} of {ok.numel()} differ, e.g. x={x[~ok][:4].tolist()}"
+        assert (got[:, seg * kp + K: (seg + 1) * kp] == 0).all(), f"segment {seg} padding"
+
+
+FP32_CHAINS = ["bias_gelu", "act_heavy", "scalars", "bcast_mul", "bias_residual", "sigmoid"]
+
+
+@pytest.mark.parametrize("chain", FP32_CHAINS)
+@pytest.mark.parametrize("shape", [(77, 200, 72), (300, 1000, 136), (130, 257, 48), (512, 520, 1000),
+                                   (64, 96, 13)], ids=lambda s: "x".join(map(str, s)))
+def test_fp32_chain_parity(chain, shape):
+    M, N, K = shape
+    dtype = torch.float32
+    a, w = _gemm_inputs(M, N, K, dtype, seed=61)
+    ops = _operands(M, N, dtype, seed=62)
+    inputs = ops + [a, w.t()]
+    left, right = len(ops), len(ops) + 1
+    steps = CHAINS[chain]
+    spec = _spec(left=left, right=right, ops=steps, out_dtype=dtype)
+    print(f"case fp32 chain={chain} shape={shape}", flush=True)
+    out = _launcher(spec, len(inputs))(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], left, right, steps)["tile"]
+    got = _np(out)
+    bad = ~np.isclose(got, ref, rtol=FP32_RTOL, atol=FP32_ATOL)
+    assert not bad.any(), f"{chain} {shape}: {bad.sum()} mismatches, max err {np.abs(got - ref).max():.3g}"
+
+
+@pytest.mark.parametrize("forced_variant", ["auto", "large", "deep3"], indirect=True)
+def test_fp32_reductions_and_escape(forced_variant):
+    """fp32 group with an escape store (bf16) and row reductions, on the
+    256-wide variants too (K' = 3 * 344 = 1032 for K = 341)."""
+    M, N, K = 600, 1030, 341
+    a, w = _gemm_inputs(M, N, K, torch.float32, seed=63)
+    bias = torch.rand(N, generator=_gen(64)) - 0.5
+    steps = [("add", 0, 1.0), ("store", 0, 1.0), ("gelu_erf", -1, 1.0)]
+    spec = _spec(left=1, right=2, ops=steps, out_dtype=torch.float32, store_tile=True,
+                 reductions=("sum", "amax", "mean"), reduce_axis=1, reduce_dtypes=(torch.float32,) * 3,
+                 extra_dtypes=(torch.bfloat16,),
+                 outputs=(("tile",), ("extra", 0), ("red", "sum"), ("red", "amax"), ("red", "mean")))
+    print(f"case fp32 reductions variant={forced_variant}", flush=True)
+    tile, pre, s, mx, mean = _launcher(spec, 3)(bias.cuda(), a.cuda(), w.t().cuda())
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(bias), _np(a), _np(w.t())], 1, 2, steps, ("sum", "amax", "mean"), 1, n_extra=1)
+    v = ref["tile"]
+    assert np.isclose(_np(tile), v, rtol=FP32_RTOL, atol=FP32_ATOL).all()
+    _check_tile(pre, ref["extra"][0], "bf16 escape of an fp32 group")
+    for got, key, scale in ((s, "sum", np.abs(v).sum(1)), (mx, "amax", np.abs(v).max(1)),
+                            (mean, "mean", np.abs(v).mean(1))):
+        err = np.abs(_np(got) - ref[key])
+        assert (err <= FP32_RTOL * np.maximum(np.abs(ref[key]), 1e-3 * scale) + 1e-6).all(), key
 
 
 # ---------------------------------------------------------------------------

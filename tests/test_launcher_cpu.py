@@ -21,9 +21,11 @@ from fuseml_amd.launcher import HipKernelLauncher
 class Recorder:
     """Stands in for the library: records each descriptor, returns `rc`."""
 
-    def __init__(self, rc=0, msg=b""):
+    def __init__(self, rc=0, msg=b"", split_rc=0):
         self.calls = []
+        self.splits = []
         self.rc = rc
+        self.split_rc = split_rc
         self.msg = msg
 
     def fuseml_gemm_epilogue(self, desc_ref, stream):
@@ -39,6 +41,11 @@ class Recorder:
         }
         self.calls.append(snap)
         return self.rc
+
+    def fuseml_split_bf16x3(self, src, rows, K, stride_r, stride_k, dst, ld_dst, k_pad, lo_mask, stream):
+        self.splits.append({"src": src.value, "rows": rows, "K": K, "sr": stride_r, "sk": stride_k,
+                            "dst": dst.value, "ld": ld_dst, "k_pad": k_pad, "mask": lo_mask})
+        return self.split_rc
 
     def fuseml_last_error(self):
         return self.msg
@@ -172,10 +179,46 @@ def test_value_errors_are_not_swallowed_by_guard():
 
 
 def test_unsupported_gemm_dtype_raises():
-    spec = EpilogueSpec(0, 1, (), torch.float32)
+    spec = EpilogueSpec(0, 1, (), torch.float64)
     launcher = make(spec, 2, Recorder())
-    with pytest.raises(_abi.FuseMLHipError, match="bf16/f16"):
-        launcher(torch.randn(4, 8), torch.randn(8, 8).t())
+    with pytest.raises(_abi.FuseMLHipError, match="bf16, f16 or fp32"):
+        launcher(torch.randn(4, 8, dtype=torch.float64), torch.randn(8, 8, dtype=torch.float64).t())
+    with pytest.raises(_abi.FuseMLHipError, match="bf16, f16 or fp32"):
+        launcher(torch.randn(4, 8), torch.randn(8, 8, dtype=BF).t())
+
+
+def test_fp32_operands_are_split_then_one_bf16_gemm():
+    """fp32 A and t(W): each is split into [M|N, 3 k_pad] bf16 parts (A as
+    hi|hi|lo, the weight rows as hi|lo|hi), and the GEMM runs on the parts
+    with K' = 3 k_pad; the epilogue and the fp32 output are unchanged."""
+    rec = Recorder()
+    M, N, K = 6, 20, 13            # K % 8 != 0: padded to 16 per segment
+    spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("relu")), torch.float32)
+    b, x, w = torch.randn(N), torch.randn(M, K), torch.randn(N, K)
+    out = make(spec, 3, rec)(b, x, w.t())
+    sa, sb = rec.splits
+    assert (sa["src"], sa["rows"], sa["K"], sa["sr"], sa["sk"], sa["mask"]) == (x.data_ptr(), M, K, K, 1, 0b100)
+    assert (sb["src"], sb["rows"], sb["K"], sb["sr"], sb["sk"], sb["mask"]) == (w.data_ptr(), N, K, K, 1, 0b010)
+    assert sa["k_pad"] == sb["k_pad"] == 16 and sa["ld"] == sb["ld"] == 48
+    c = rec.calls[0]
+    assert (c["M"], c["N"], c["K"], c["lda"], c["ldb"], c["ab"]) == (M, N, 48, 48, 48, _abi.BF16)
+    assert c["a"] == sa["dst"] and c["b"] == sb["dst"]
+    assert c["operands"] == [(0, 1, N, _abi.F32)] and c["out"] == (True, N, _abi.F32)
+    assert out.dtype == torch.float32 and out.shape == (M, N)
+    # strided K: the split reads the operand in place, whatever its strides
+    n_before = len(rec.splits)
+    x2 = torch.randn(M, 2 * K)[:, ::2]
+    make(spec, 3, rec)(b, x2, w.t())
+    sa2 = rec.splits[n_before]
+    assert (sa2["src"], sa2["sr"], sa2["sk"]) == (x2.data_ptr(), 2 * K, 2)
+
+
+def test_fp32_split_error_is_a_hip_error():
+    rec = Recorder(split_rc=_abi.EINVAL, msg=b"split_bf16x3: bad sizes")
+    spec = EpilogueSpec(0, 1, (), torch.float32)
+    with pytest.raises(_abi.FuseMLHipError, match="bad sizes"):
+        make(spec, 2, rec)(torch.randn(4, 8), torch.randn(8, 8).t())
+    assert rec.calls == []
 
 
 def test_name_for_fx():
