@@ -26,6 +26,9 @@ Rank 0 prints one JSON line carrying:
   output at sampled rows against a float32 PyTorch reference (tiles rtol/atol
   2e-2, reductions 1e-2 relative; bench_mlp_block.py:453-485), with eager
   bf16's own error beside it as calibration;
+* ``fp32_block`` — the C2 block in fp32 (not a benchmark config): compiled,
+  both groups as bf16 split products, against eager fp32, with errors
+  against float64 at sampled rows;
 * ``cpu_baseline`` — the same eager module on this host's CPU cores (bf16,
   full batch, all cores, median of timed forwards): the reference's eager
   path, reported, not a target.
@@ -76,6 +79,7 @@ def _parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-eager", action="store_true", help="skip the eager GPU comparison")
     p.add_argument("--no-compile", action="store_true", help="skip torch.compile timing")
+    p.add_argument("--no-fp32", action="store_true", help="skip the fp32 block (split-product path)")
     p.add_argument("--eager-only", action="store_true",
                    help="run only the eager leg of --workload (rocprof counter runs of the eager module)")
     p.add_argument("--cpu-iters", type=int, default=5)
@@ -373,6 +377,47 @@ def _config_detail(name, args, dev, peak_tflops, flush):
             comp["check"] = _check(_as_parts(name, co), ref, rows)
             out["compiled"] = comp
     del wl, stages, st0, last
+    torch.cuda.empty_cache()
+    return out
+
+
+def _fp32_block(args, dev):
+    """The C2 block in fp32 (not a benchmark config: an fp32 model's path).
+    The reference fuses fp32 groups through Triton's tf32 dot
+    (kernel_generator.py:1536); here both groups run as three-term bf16 split
+    products (fuseml_split_bf16x3 + the fused kernel).  Compiled module against
+    the same module in eager fp32 (`allow_tf32` off), HIP-event medians, and
+    both against a float64 reference at sampled rows."""
+    from fuseml_amd.compiler import FuseMLCompiler
+    from fuseml_amd.workloads import TransformerMLP
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.manual_seed(0)
+    m = TransformerMLP(1024, 4096).eval().to(dev)
+    x = torch.randn(16384, 1024, generator=torch.Generator().manual_seed(1)).to(dev)
+    rows = _sample_rows(16384)
+    with torch.no_grad():
+        xr = x[rows.to(dev)].double().cpu()
+        w1, b1 = m.linear1.weight.double().cpu(), m.linear1.bias.double().cpu()
+        w2, b2 = m.linear2.weight.double().cpu(), m.linear2.bias.double().cpu()
+        ref = torch.nn.functional.gelu(xr @ w1.t() + b1) @ w2.t() + b2 + xr
+        torch._dynamo.reset()
+        be = FuseMLCompiler()
+        compiled = torch.compile(m, backend=be)
+        y = compiled(x)
+        ye = m(x)
+        torch.cuda.synchronize()
+        out = {"workload": "TransformerMLP fp32: x[16384,1024] -> 4096 -> 1024 + residual",
+               "fusion_strategy": be.fusion_strategy,
+               "hip_launchers": len({id(l) for l in be.launchers})}
+        out["compiled"] = _time_events(lambda: compiled(x), args)
+        out["eager_fp32"] = _time_events(lambda: m(x), args)
+    out["speedup_vs_eager"] = round(out["eager_fp32"]["median_ms"] / out["compiled"]["median_ms"], 3)
+    err = lambda t: float((t[rows.to(dev)].double().cpu() - ref).abs().max())  # noqa: E731
+    out["max_abs_err_vs_f64"] = {"compiled": err(y), "eager_fp32": err(ye)}
+    flops = 2.0 * 16384 * 1024 * 4096 * 2
+    out["tflops_equivalent"] = round(flops / (out["compiled"]["median_ms"] * 1e-3) / 1e12, 1)
+    del m, x, compiled, y, ye
     torch.cuda.empty_cache()
     return out
 
@@ -728,6 +773,10 @@ def main():
         configs[c] = _config_detail(c, args, dev, peak["tflops"], flush)
     del flush
     torch.cuda.empty_cache()
+    fp32 = None
+    if args.configs and not args.no_fp32:
+        print("[bench] fp32 block", file=sys.stderr, flush=True)
+        fp32 = _fp32_block(args, dev)
 
     cpu = None
     if not args.no_cpu:
@@ -778,6 +827,7 @@ def main():
         # the all-HIP pipeline's HBM bytes against the eager module's (committed counter summaries)
         "hbm_traffic": _hbm_traffic(name, [tuple(g) for g in _gemms_of(name)]),
         "configs": configs,
+        "fp32_block": fp32,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
