@@ -559,6 +559,43 @@ def test_split_bf16x3_bit_exact(layout, lo_mask):
         assert (got[:, seg * kp + K: (seg + 1) * kp] == 0).all(), f"segment {seg} padding"
 
 
+def test_fp32_graph_capture_replays():
+    """An fp32 group is three launches (two splits, then the GEMM) with its
+    split buffers from the caching allocator: captured in a HIP graph, each
+    replay with new inputs copied in equals an eager launch bit for bit."""
+    M, N, K = 600, 1030, 341
+    spec = _spec(left=1, right=2, ops=[("add", 0, 1.0), ("gelu_erf", -1, 1.0)], out_dtype=torch.float32)
+    L = _launcher(spec, 3)
+
+    def host_inputs(seed):
+        a, w = _gemm_inputs(M, N, K, torch.float32, seed=seed)
+        return [torch.rand(N, generator=_gen(seed + 2)) - 0.5, a, w.t()]
+
+    print("case fp32 graph capture", flush=True)
+    static = [t.cuda() for t in host_inputs(70)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        L(*static)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g_out = L(*static)
+    for seed in (71, 72):
+        host = host_inputs(seed)
+        for dst, src in zip(static, host):
+            dst.copy_(src)
+        eager = L(*static)
+        torch.cuda.synchronize()
+        g_out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, eager), f"replay seed {seed} differs from eager"
+        ref = ora.gemm_epilogue([_np(t) for t in host], 1, 2, [("add", 0, 1.0), ("gelu_erf", -1, 1.0)])["tile"]
+        assert np.isclose(_np(g_out), ref, rtol=FP32_RTOL, atol=FP32_ATOL).all()
+
+
 FP32_CHAINS = ["bias_gelu", "act_heavy", "scalars", "bcast_mul", "bias_residual", "sigmoid"]
 
 
