@@ -232,9 +232,17 @@ class HipKernelLauncher:
             inputs = tuple(t.contiguous() if isinstance(t, torch.Tensor) else t for t in inputs)
         M, N = plan.M, plan.N
         a, b = inputs[spec.left], inputs[spec.right]
+        dev = a.device
+        if isinstance(self._lib, ctypes.CDLL):
+            # The kernels dereference every pointer on the GPU: a host tensor or
+            # one on another device would fault there.  Raised before any HIP
+            # call, as a recoverable error (Triton raises for CPU tensors too).
+            if dev.type != "cuda" or any(inputs[i].device != dev for i in self._used):
+                raise _abi.FuseMLHipError(
+                    _abi.EINVAL, f"inputs on {sorted({str(inputs[i].device) for i in self._used})}: "
+                    "every tensor must be on the launch's GPU")
         if not plan.k_split:
             a, b = _k_major_left(a), _k_major_right(b)
-        dev = a.device
 
         tile = None
         if spec.store_tile:

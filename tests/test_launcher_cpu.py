@@ -333,3 +333,18 @@ def test_new_signature_gets_its_own_plan():
     launcher(torch.randn(40, 16, dtype=BF), torch.randn(24, 16, dtype=BF).t())
     assert len(launcher._plans) == 2
     assert [(c["M"], c["N"], c["K"]) for c in rec.calls] == [(8, 24, 16), (40, 24, 16)]
+
+
+def test_host_tensors_are_refused_before_any_device_call():
+    """With the real library bound, CPU tensors (or tensors on different
+    devices) raise a recoverable error instead of reaching a kernel that would
+    dereference host pointers on the GPU; the eager guard then takes over."""
+    spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("relu")), BF)
+    b, x, w = torch.randn(16, dtype=BF), torch.randn(8, 32, dtype=BF), torch.randn(16, 32, dtype=BF)
+    launcher = HipKernelLauncher(spec, 3)                   # the real library (loads without a GPU)
+    assert isinstance(launcher._lib, ctypes.CDLL)
+    with pytest.raises(_abi.FuseMLHipError, match="must be on the launch's GPU"):
+        launcher(b, x, w.t())
+    guarded = HipKernelLauncher(spec, 3, eager_fn=lambda bb, xx, ww: torch.relu(torch.addmm(bb, xx, ww)))
+    out = guarded(b, x, w.t())
+    assert guarded.fallback_count == 1 and torch.equal(out, torch.relu(torch.addmm(b, x, w.t())))
