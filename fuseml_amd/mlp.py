@@ -82,6 +82,11 @@ class HipMlpLauncher:
         dt = x.dtype
         if dt not in _DTYPES or any(t is not None and t.dtype != dt for t in (w1t, b1, w2t, b2, r)):
             raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "mlp_block: every tensor must share one bf16/f16 dtype")
+        tensors = [t for t in (x, w1t, b1, w2t, b2, r) if t is not None]
+        if isinstance(self._lib, ctypes.CDLL) and (x.device.type != "cuda" or
+                                                   any(t.device != x.device for t in tensors)):
+            # a host pointer (or another device's) would fault in the kernel
+            raise _abi.FuseMLHipError(_abi.EINVAL, "mlp_block: every tensor must be on the launch's GPU")
         if tuple(w1t.shape) != (D, I) or tuple(w2t.shape) != (I, D) or b1.shape != (I,) or \
                 (b2 is not None and b2.shape != (D,)) or (r is not None and tuple(r.shape) != (M, D)):
             raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "mlp_block: operand shapes do not chain")

@@ -118,3 +118,15 @@ def test_mlp_shape_rule():
     assert not mlp_shape_supported(8192, 4096, 16384, BF)[0]      # C5: D too wide
     assert not mlp_shape_supported(64, 512, 100, BF)[0]           # I % 32
     assert not mlp_shape_supported(64, 512, 1024, torch.float32)[0]
+
+
+def test_mlp_launcher_refuses_host_tensors():
+    """With the real library bound, CPU tensors raise before any device call."""
+    D, I, M = 256, 64, 8
+    x = torch.randn(M, D, dtype=BF)
+    w1t, w2t = torch.randn(I, D, dtype=BF).t(), torch.randn(D, I, dtype=BF).t()
+    b1, b2 = torch.randn(I, dtype=BF), torch.randn(D, dtype=BF)
+    launcher = HipMlpLauncher()
+    assert isinstance(launcher._lib, ctypes.CDLL)
+    with pytest.raises(_abi.FuseMLHipError, match="must be on the launch's GPU"):
+        launcher(x, w1t, b1, w2t, b2, x)
