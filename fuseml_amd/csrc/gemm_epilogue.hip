@@ -423,8 +423,13 @@ __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, 
 // two per SIMD), 3 one wave per SIMD (4 waves, 128x128 wave tiles, accumulators
 // in AGPRs) with two deep stages (BK=64), the barrier before each stage's last
 // k-step and each stage's DMA split over two k-steps, 6 the same tile with a
-// whole stage of fragments in registers (described at its loop).
-template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T>
+// whole stage of fragments in registers (described at its loop).  RED: the
+// launch has reductions, and the row partials of interior tiles take an
+// unmasked tree.  Only that path differs between the two instantiations: a
+// kernel built without the reductions' code gets an s_waitcnt vmcnt(0) in the
+// one-wave K loop, and extra code in the shared epilogue moves every kernel's
+// block layout by a few per cent.
+template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T, bool RED>
 __global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED >= 3 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   using G = StageGeom<BK>;
@@ -1108,6 +1113,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     const int nw = n0 + wn * TN + 4 * khalf;
     const bool row_red = d.reduce_mask != 0 && d.reduce_axis == 1;
     const bool col_red = d.reduce_mask != 0 && d.reduce_axis == 0;
+    const bool interior = m0 + BM <= M && n0 + BN <= N;  // every element of the tile in range
     const int crow = tid / CPR;  // cooperative-pass row and chunk of this thread
     const int cchk = tid % CPR;
 
@@ -1361,8 +1367,26 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         }
         // Partial reductions exclude every element outside [0,M) x [0,N) (the
         // reference lets padded tile elements through, kernel_generator.py:1959-1960,
-        // 1983-1984).
-        if (row_red || col_red) {
+        // 1983-1984).  Row partials of an interior tile need no masks: the
+        // lane's 16 values of the row are summed (and maxed) as a pairwise tree,
+        // four dependent steps instead of a 16-long chain.
+        if (RED && row_red && interior) {
+          float s8[8], m8[8];
+          static_for<0, 8>([&](auto e) {
+            s8[e] = A[j][2 * e] + A[j][2 * e + 1];
+            m8[e] = max_nan(A[j][2 * e], A[j][2 * e + 1]);
+          });
+          static_for<0, 4>([&](auto e) {
+            s8[e] = s8[2 * e] + s8[2 * e + 1];
+            m8[e] = max_nan(m8[2 * e], m8[2 * e + 1]);
+          });
+          static_for<0, 2>([&](auto e) {
+            s8[e] = s8[2 * e] + s8[2 * e + 1];
+            m8[e] = max_nan(m8[2 * e], m8[2 * e + 1]);
+          });
+          rs[j] += s8[0] + s8[1];
+          rmx[j] = max_nan(rmx[j], max_nan(m8[0], m8[1]));
+        } else if (row_red || col_red) {
           static_for<0, 16>([&](auto r) {
             const int n = nb + 8 * (r >> 2) + (r & 3);
             const bool in = (m < M) && (n < N);
@@ -1748,12 +1772,19 @@ hipError_t launch_variant(const fuseml_gemm_desc& d, hipStream_t stream, int max
   int64_t tiles = cdiv(d.M, C.bm) * cdiv(d.N, C.bn);
   if (max_wg > 0 && tiles > max_wg) tiles = max_wg;
   const dim3 grid((unsigned)tiles), block(C.wm * C.wn * 64);
-  if (d.ab_dtype == FUSEML_BF16)
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16>), grid,
+  const bool red = d.reduce_mask != 0;
+  if (d.ab_dtype == FUSEML_BF16 && !red)
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16, false>), grid,
                        block, 0, stream, d);
+  else if (d.ab_dtype == FUSEML_BF16)
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16, true>), grid,
+                       block, 0, stream, d);
+  else if (!red)
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, _Float16, false>),
+                       grid, block, 0, stream, d);
   else
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, _Float16>), grid,
-                       block, 0, stream, d);
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, _Float16, true>),
+                       grid, block, 0, stream, d);
   return hipGetLastError();
 }
 

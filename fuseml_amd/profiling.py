@@ -36,6 +36,7 @@ from __future__ import annotations
 import argparse
 import csv
 import json
+import re
 import statistics
 import sys
 from collections import defaultdict
@@ -46,12 +47,13 @@ PROBE_KERNEL_HINT = "mfma_peak_kernel"
 
 
 def _short(name: str) -> str:
-    """gemm_epilogue_kernel<BM,BN,BK,S,WM,WN,SCHED,dtype> from the mangled name."""
-    if "gemm_epilogue_kernel" in name and "ILi" in name:
-        args = name[name.index("ILi") + 3:].split("EEv")[0]
-        ints, _, tail = args.rpartition("E")
-        dtype = {"DF16b": "bf16", "DF16_": "f16"}.get(tail, tail)
-        return "gemm_epilogue_kernel<" + ints.replace("ELi", ",") + "," + dtype + ">"
+    """gemm_epilogue_kernel<BM,BN,BK,S,WM,WN,SCHED,dtype[,red]> from the mangled
+    name (",red": the instantiation that carries the reductions)."""
+    m = re.search(r"gemm_epilogue_kernelI((?:Li\d+E)+)(DF16b|DF16_)(?:Lb([01])E)?E", name)
+    if m:
+        ints = ",".join(re.findall(r"Li(\d+)E", m.group(1)))
+        dtype = {"DF16b": "bf16", "DF16_": "f16"}[m.group(2)]
+        return f"gemm_epilogue_kernel<{ints},{dtype}{',red' if m.group(3) == '1' else ''}>"
     return name[:60]
 
 

@@ -95,3 +95,15 @@ def test_step_traffic_totals_every_kernel_per_call(tmp_path):
     k = {r["kernel"]: r for r in t["kernels"]}
     assert not k["fillBuffer"]["per_call"] and k["elementwise"]["per_call"]
     assert k["Cijk_gemm"]["dispatches"] == 6 and abs(k["Cijk_gemm"]["fetch_bytes_per_call"] - 150.0 * 2048) < 1e-6
+
+
+def test_kernel_names_with_the_reduction_flag():
+    """The kernel template carries a bool (launch with reductions): the short
+    name keeps the shape and dtype, and marks the reduction instantiation."""
+    from fuseml_amd.profiling import _short
+
+    base = "_ZN12_GLOBAL__N_120gemm_epilogue_kernelILi256ELi256ELi64ELi2ELi2ELi2ELi6E"
+    assert _short(base + "DF16bLb0EEEv16fuseml_gemm_desc") == "gemm_epilogue_kernel<256,256,64,2,2,2,6,bf16>"
+    assert _short(base + "DF16_Lb1EEEv16fuseml_gemm_desc") == "gemm_epilogue_kernel<256,256,64,2,2,2,6,f16,red>"
+    assert _short(GEMM) == "gemm_epilogue_kernel<256,256,32,4,2,4,1,bf16>"
+    assert _short("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
