@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY (see ``oracle/gemm_epilogue.py``): used by tests/,
 ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg.
 
-Each function is the eager module of one BASELINE config written as array
+Each function is the eager module of one benchmark config written as array
 arithmetic on weights in ``nn.Linear`` layout ``W[out, in]`` (``y = x W^T + b``):
 
 * C1/C2 ``transformer_mlp`` — benchmarks/bench_mlp_block.py:160-182

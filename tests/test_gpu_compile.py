@@ -1,6 +1,6 @@
 """End to end on the GPU: torch.compile(model, backend=FuseMLCompiler()).
 
-Each workload (BASELINE configs C1-C5; M scaled down so the float64 oracle
+Each workload (benchmark configs C1-C5; M scaled down so the float64 oracle
 stays fast, every other dimension at full size) is compiled, run under
 no_grad, and compared with the CPU oracle on the same bf16 inputs.  The test
 also asserts that the fused HIP launchers actually ran (no silent eager path).

@@ -2,7 +2,7 @@
 need real sizes: the reference's own FusionGroup on the device, NaN
 propagation, operands beyond 2 GiB.
 
-Every config runs at exactly its BASELINE shape, so the kernel variant and the
+Every config runs at exactly its benchmark shape, so the kernel variant and the
 number of persistent rounds are the ones the benchmark measures (C3: 1024
 tiles of 256x256 on the ping-pong schedule; C4: 1024 tiles, K=2048, the
 one-wave whole-stage schedule, a stored tile plus three fp32 row reductions;
