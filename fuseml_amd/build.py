@@ -1,13 +1,16 @@
 """Build the gfx950 HIP kernel library in-tree: ``python -m fuseml_amd.build``.
 
-One ``hipcc`` invocation compiles ``fuseml_amd/csrc/*.hip`` into
-``fuseml_amd/libfuseml_hip.so`` for ``--offload-arch=gfx950`` only.  The build
-is ahead-of-time: there is no runtime JIT (the reference compiles Triton
-kernels on the first call, fuseml/codegen/kernel_generator.py:1067-1172).
+Each ``fuseml_amd/csrc/*.hip`` is compiled by its own ``hipcc -c`` for
+``--offload-arch=gfx950`` only (in parallel: the GEMM kernels are split one
+tile variant per translation unit), and the objects are linked into
+``fuseml_amd/libfuseml_hip.so``.  The build is ahead-of-time: there is no
+runtime JIT (the reference compiles Triton kernels on the first call,
+fuseml/codegen/kernel_generator.py:1067-1172).
 """
 
 from __future__ import annotations
 
+import concurrent.futures
 import glob
 import os
 import shutil
@@ -19,6 +22,7 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 CSRC_DIR = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libfuseml_hip.so")
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
 
 ARCH = "gfx950"
 
@@ -28,9 +32,10 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# hipcc's host pass does not know the packed-fp32 feature and says so.
+_NOISE = "packed-fp32-ops' is not a recognized feature"
 
 
 def hipcc() -> str:
@@ -44,23 +49,32 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC_DIR, "*.hip")))
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into the in-tree shared library; return its path."""
-    srcs = sources()
-    if not srcs:
-        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", *srcs, "-o", tmp]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass does not know the packed-fp32 feature and says so; drop that noise.
-    noise = "packed-fp32-ops' is not a recognized feature"
-    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in proc.stderr.splitlines() if _NOISE not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every HIP source and link the in-tree shared library; return its path."""
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    cc = hipcc()
+    objs = [os.path.join(OBJ_DIR, os.path.splitext(os.path.basename(s))[0] + ".o") for s in srcs]
+    cmds = [[cc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-c", s, "-o", o] for s, o in zip(srcs, objs)]
+    workers = jobs or min(len(cmds), max(1, len(os.sched_getaffinity(0))), 16)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        for f in [pool.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    tmp = LIB_PATH + ".tmp"
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
