@@ -54,6 +54,17 @@ def _short(name: str) -> str:
         ints = ",".join(re.findall(r"Li(\d+)E", m.group(1)))
         dtype = {"DF16b": "bf16", "DF16_": "f16"}[m.group(2)]
         return f"gemm_epilogue_kernel<{ints},{dtype}{',red' if m.group(3) == '1' else ''}>"
+    # Demangled by the profiler: "void ns::gemm_epilogue_kernel<256, 256, ..., __bf16, true>(...)".
+    # rocprofv3 demangles some instantiations with a garbled type tail (the
+    # __bf16 mangling); then only the seven tile integers are kept.
+    m = re.search(r"gemm_epilogue_kernel<((?:\d+, ){6}\d+), ([^()]*)>\(", name)
+    if m:
+        ints = m.group(1).replace(" ", "")
+        tail = [t.strip() for t in m.group(2).split(",")]
+        dtype = {"__bf16": "bf16", "_Float16": "f16"}.get(tail[0]) if tail else None
+        if dtype is None or len(tail) != 2 or tail[1] not in ("true", "false"):
+            return f"gemm_epilogue_kernel<{ints},...>"
+        return f"gemm_epilogue_kernel<{ints},{dtype}{',red' if tail[1] == 'true' else ''}>"
     return name[:60]
 
 

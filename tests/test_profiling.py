@@ -107,3 +107,17 @@ def test_kernel_names_with_the_reduction_flag():
     assert _short(base + "DF16_Lb1EEEv16fuseml_gemm_desc") == "gemm_epilogue_kernel<256,256,64,2,2,2,6,f16,red>"
     assert _short(GEMM) == "gemm_epilogue_kernel<256,256,32,4,2,4,1,bf16>"
     assert _short("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
+
+
+def test_kernel_names_demangled_by_the_profiler():
+    """rocprofv3 demangles some instantiations (named namespace): the short name
+    is the same as for the mangled form, and a garbled type tail keeps only the
+    tile integers."""
+    from fuseml_amd.profiling import _short
+
+    named = "_ZN11fuseml_gemm20gemm_epilogue_kernelILi256ELi256ELi32ELi4ELi2ELi4ELi1EDF16bLb0EEEv16fuseml_gemm_desc"
+    assert _short(named) == "gemm_epilogue_kernel<256,256,32,4,2,4,1,bf16>"
+    dem = "void fuseml_gemm::gemm_epilogue_kernel<256, 256, 64, 2, 2, 2, 6, __bf16, true>(fuseml_gemm_desc)"
+    assert _short(dem) == "gemm_epilogue_kernel<256,256,64,2,2,2,6,bf16,red>"
+    garbled = "void fuseml_gemm::gemm_epilogue_kernel<256, 256, 64, 2, 2, 2, 6, bool _Accum, bool, E>(fuseml_gemm_desc)"
+    assert _short(garbled) == "gemm_epilogue_kernel<256,256,64,2,2,2,6,...>"
