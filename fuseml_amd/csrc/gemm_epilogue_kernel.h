@@ -458,12 +458,18 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     const int in_round = min(nwg, ntiles - round0);
     int lid = tile;
     if ((in_round & 7) == 0) lid = round0 + ((int)blockIdx.x & 7) * (in_round >> 3) + ((int)blockIdx.x >> 3);
+    // The previous tile's LDS reads and global stores are complete in every
+    // wave before this tile's DMA overwrites the slots.  The waits run on every
+    // path into the tile (on the first tile nothing is outstanding): behind a
+    // branch, the compiler's wait insertion sees the previous tile's last DMAs
+    // as possibly pending at this tile's K loop (their VGPR offsets
+    // overwritten by fragment reads there) and puts an s_waitcnt vmcnt(0) into
+    // the steady loop.
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkmcnt0();
+    wait_vmcnt<0>();
+    __builtin_amdgcn_sched_barrier(0);
     if (tile != (int)blockIdx.x) {
-      // The previous tile's LDS reads and global stores are complete in every
-      // wave before this tile's DMA overwrites the slots.
-      __builtin_amdgcn_sched_barrier(0);
-      wait_lgkmcnt0();
-      wait_vmcnt<0>();
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
@@ -1317,7 +1323,33 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       const int khalf = ln >> 5;
       const int mw = m0 + wm * TM + l32;
       const int nw = n0 + wn * TN + 4 * khalf;
-      static_for<0, NJ>([&](auto j) {
+      // Without reductions, a staged output is all the block's tail does: the
+      // staging writes of its NJ row blocks under one dtype branch, and no
+      // bookkeeping of the other paths on the way.
+      if (!RED && use_stage_out) {
+        const int u0 = (wn * TN + 32 * i) / 4 + khalf;
+        if (out_bf16) {
+          static_for<0, NJ>([&](auto j) {
+            const int r_loc = wm * TM + 32 * j + l32;
+            static_for<0, 4>([&](auto g) {
+              const f32x16_t& v = A[j];
+              *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
+                  make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
+            });
+          });
+          asm volatile("; staged output block, bf16");
+        } else {
+          static_for<0, NJ>([&](auto j) {
+            const int r_loc = wm * TM + 32 * j + l32;
+            static_for<0, 4>([&](auto g) {
+              const f32x16_t& v = A[j];
+              *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
+                  make_uint2(pack_f16x2(v[4 * g], v[4 * g + 1]), pack_f16x2(v[4 * g + 2], v[4 * g + 3]));
+            });
+          });
+          asm volatile("; staged output block, fp16");
+        }
+      } else static_for<0, NJ>([&](auto j) {
         const int m = mw + 32 * j;
         const int nb = nw + 32 * i;
         if (use_stage_out) {
@@ -1371,7 +1403,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           });
           rs[j] += s8[0] + s8[1];
           rmx[j] = max_nan(rmx[j], max_nan(m8[0], m8[1]));
-        } else if (row_red || col_red) {
+        } else if (RED && (row_red || col_red)) {
           static_for<0, 16>([&](auto r) {
             const int n = nb + 8 * (r >> 2) + (r & 3);
             const bool in = (m < M) && (n < N);
@@ -1387,7 +1419,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           });
         }
       });
-      if (col_red) {
+      if (RED && col_red) {
         // Column partials: reduce over the 32 rows held by each half-wave.  Column
         // reductions use neither a staged output nor a staged operand (the host
         // does not flag them), so the staging tile's LDS is free here.
@@ -1464,7 +1496,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       }
     }
 
-    if (d.reduce_mask == 0) continue;
+    if (!RED || d.reduce_mask == 0) continue;
     if (row_red) {
       // The partials overwrite the staging tile, which other waves may still be
       // draining (staged output) or reading (staged operand).
