@@ -409,11 +409,9 @@ __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, 
 // in AGPRs) with two deep stages (BK=64), the barrier before each stage's last
 // k-step and each stage's DMA split over two k-steps, 6 the same tile with a
 // whole stage of fragments in registers (described at its loop).  RED: the
-// launch has reductions, and the row partials of interior tiles take an
-// unmasked tree.  Only that path differs between the two instantiations: a
-// kernel built without the reductions' code gets an s_waitcnt vmcnt(0) in the
-// one-wave K loop, and extra code in the shared epilogue moves every kernel's
-// block layout by a few per cent.
+// launch has reductions.  Only that instantiation carries the reductions' code
+// (the row partials of interior tiles as an unmasked tree); without it, a
+// staged output's block tail is the staging writes alone.
 template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T, bool RED>
 __global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED >= 3 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
