@@ -1321,10 +1321,12 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       const int khalf = ln >> 5;
       const int mw = m0 + wm * TM + l32;
       const int nw = n0 + wn * TN + 4 * khalf;
-      // Without reductions, a staged output is all the block's tail does: the
-      // staging writes of its NJ row blocks under one dtype branch, and no
-      // bookkeeping of the other paths on the way.
-      if (!RED && use_stage_out) {
+      // The block's NJ row blocks into the staged output under one dtype
+      // branch (or stored unstaged), then the reduction partials, each kind for
+      // all row blocks at once: branches per row block would keep the row
+      // blocks' independent work in separate basic blocks, which at one wave
+      // per SIMD leaves every dependent step's latency exposed.
+      if (use_stage_out) {
         const int u0 = (wn * TN + 32 * i) / 4 + khalf;
         if (out_bf16) {
           static_for<0, NJ>([&](auto j) {
@@ -1347,76 +1349,60 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
           });
           asm volatile("; staged output block, fp16");
         }
-      } else static_for<0, NJ>([&](auto j) {
-        const int m = mw + 32 * j;
-        const int nb = nw + 32 * i;
-        if (use_stage_out) {
-          const int r_loc = wm * TM + 32 * j + l32;
-          const int u0 = (wn * TN + 32 * i) / 4 + khalf;
-          // One uniform branch per row block and one packed conversion per two
-          // values.  The arms end in different asm markers, so the compiler does
-          // not merge their LDS writes into one write of selected values (which
-          // the back end would split again into a branch per value).
-          if (out_bf16) {
-            static_for<0, 4>([&](auto g) {
-              const f32x16_t& v = A[j];
-              *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
-                  make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
-            });
-            asm volatile("; staged output, bf16");
-          } else {
-            static_for<0, 4>([&](auto g) {
-              const f32x16_t& v = A[j];
-              *reinterpret_cast<uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g)) =
-                  make_uint2(pack_f16x2(v[4 * g], v[4 * g + 1]), pack_f16x2(v[4 * g + 2], v[4 * g + 3]));
-            });
-            asm volatile("; staged output, fp16");
-          }
-        }
-        if (d.out.ptr != nullptr && !use_stage_out) {
+      } else if (d.out.ptr != nullptr) {
+        static_for<0, NJ>([&](auto j) {
+          const int m = mw + 32 * j;
+          const int nb = nw + 32 * i;
           static_for<0, 4>([&](auto g) {
-            const float x[4] = {A[j][4 * g], A[j][4 * g + 1], A[j][4 * g + 2],
-                                A[j][4 * g + 3]};
+            const float x[4] = {A[j][4 * g], A[j][4 * g + 1], A[j][4 * g + 2], A[j][4 * g + 3]};
             store_out4(d.out, m, nb + 8 * g, M, N, x);
           });
+        });
+      }
+      // Partial reductions exclude every element outside [0,M) x [0,N) (the
+      // reference lets padded tile elements through, kernel_generator.py:1959-1960,
+      // 1983-1984).  Row partials of an interior tile need no masks: each row
+      // block's 16 values of the row are summed (and maxed) as a pairwise tree,
+      // four dependent steps instead of a 16-long chain.
+      if constexpr (RED) {
+        if (row_red && interior) {
+          static_for<0, NJ>([&](auto j) {
+            float s8[8], m8[8];
+            static_for<0, 8>([&](auto e) {
+              s8[e] = A[j][2 * e] + A[j][2 * e + 1];
+              m8[e] = max_nan(A[j][2 * e], A[j][2 * e + 1]);
+            });
+            static_for<0, 4>([&](auto e) {
+              s8[e] = s8[2 * e] + s8[2 * e + 1];
+              m8[e] = max_nan(m8[2 * e], m8[2 * e + 1]);
+            });
+            static_for<0, 2>([&](auto e) {
+              s8[e] = s8[2 * e] + s8[2 * e + 1];
+              m8[e] = max_nan(m8[2 * e], m8[2 * e + 1]);
+            });
+            rs[j] += s8[0] + s8[1];
+            rmx[j] = max_nan(rmx[j], max_nan(m8[0], m8[1]));
+          });
+        } else if (row_red || col_red) {
+          static_for<0, NJ>([&](auto j) {
+            const int m = mw + 32 * j;
+            const int nb = nw + 32 * i;
+            static_for<0, 16>([&](auto r) {
+              const int n = nb + 8 * (r >> 2) + (r & 3);
+              const bool in = (m < M) && (n < N);
+              const float x = A[j][(int)r];
+              if (row_red && in) {
+                rs[j] += x;
+                rmx[j] = max_nan(rmx[j], x);
+              }
+              if (col_red && in) {
+                cs[r] += x;
+                cmx[r] = max_nan(cmx[r], x);
+              }
+            });
+          });
         }
-        // Partial reductions exclude every element outside [0,M) x [0,N) (the
-        // reference lets padded tile elements through, kernel_generator.py:1959-1960,
-        // 1983-1984).  Row partials of an interior tile need no masks: the
-        // lane's 16 values of the row are summed (and maxed) as a pairwise tree,
-        // four dependent steps instead of a 16-long chain.
-        if (RED && row_red && interior) {
-          float s8[8], m8[8];
-          static_for<0, 8>([&](auto e) {
-            s8[e] = A[j][2 * e] + A[j][2 * e + 1];
-            m8[e] = max_nan(A[j][2 * e], A[j][2 * e + 1]);
-          });
-          static_for<0, 4>([&](auto e) {
-            s8[e] = s8[2 * e] + s8[2 * e + 1];
-            m8[e] = max_nan(m8[2 * e], m8[2 * e + 1]);
-          });
-          static_for<0, 2>([&](auto e) {
-            s8[e] = s8[2 * e] + s8[2 * e + 1];
-            m8[e] = max_nan(m8[2 * e], m8[2 * e + 1]);
-          });
-          rs[j] += s8[0] + s8[1];
-          rmx[j] = max_nan(rmx[j], max_nan(m8[0], m8[1]));
-        } else if (RED && (row_red || col_red)) {
-          static_for<0, 16>([&](auto r) {
-            const int n = nb + 8 * (r >> 2) + (r & 3);
-            const bool in = (m < M) && (n < N);
-            const float x = A[j][(int)r];
-            if (row_red && in) {
-              rs[j] += x;
-              rmx[j] = max_nan(rmx[j], x);
-            }
-            if (col_red && in) {
-              cs[r] += x;
-              cmx[r] = max_nan(cmx[r], x);
-            }
-          });
-        }
-      });
+      }
       if (RED && col_red) {
         // Column partials: reduce over the 32 rows held by each half-wave.  Column
         // reductions use neither a staged output nor a staged operand (the host
