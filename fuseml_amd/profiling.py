@@ -25,6 +25,9 @@ aggregation over XCDs, CUs and SIMDs) cancels.  It also reports each launch's
 clock, GRBM_GUI_ACTIVE per XCD over the traced duration when a kernel trace
 of the same run is given.
 
+``counters`` averages every counter of one ``--pmc`` pass per launch, also per
+wave of the dispatch (instruction counts, LDS bank conflicts, active cycles).
+
 ``step-traffic`` sums the same counters over every dispatch of a run (the
 calibration copy aside) and divides by ``--calls``, the number of times the
 run called the module (``bench.py --eager-only`` prints it): HBM bytes per
@@ -159,6 +162,27 @@ def mfma_busy_summary(pmc_csv: str, per_step: int = 1, xcds: int = 8) -> Dict[st
     return {"probe_ratio": ref, "kernels": kernels}
 
 
+def counter_summary(pmc_csv: str, per_step: int = 1) -> Dict[str, object]:
+    """Mean of every counter of one ``--pmc`` pass per (kernel, launch), and
+    per wave of the dispatch (grid / 64): e.g. VALU and LDS instruction counts,
+    LDS bank-conflict cycles, active-VALU cycles of the fused kernels."""
+    rows = list(csv.DictReader(open(pmc_csv)))
+    names = sorted({r["Counter_Name"] for r in rows})
+    out: Dict[Tuple[str, int, int], Dict[str, object]] = {}
+    for c in names:
+        for key, vals in counter_by_dispatch(pmc_csv, c, per_step).items():
+            name, grid, p = key
+            if COPY_KERNEL_HINT in name:
+                continue
+            e = out.setdefault(key, {"kernel": "mfma_peak_kernel (probe)" if PROBE_KERNEL_HINT in name else _short(name),
+                                     "grid": grid, "launch": p, "dispatches": len(vals), "counters": {},
+                                     "per_wave": {}})
+            e["counters"][c] = statistics.mean(vals)
+            if grid:
+                e["per_wave"][c] = round(statistics.mean(vals) / (grid / 64), 1)
+    return {"counters": names, "kernels": [out[k] for k in sorted(out)]}
+
+
 def step_traffic(fetch_csv: str, write_csv: str, copy_mib: float, calls: int) -> Dict[str, object]:
     """HBM bytes per call of a whole module (every dispatch but the calibration
     copy), for a run that called the module ``calls`` times: totals over the
@@ -206,6 +230,9 @@ def main(argv=None) -> int:
     mb = sub.add_parser("mfma-busy")
     mb.add_argument("csv")
     mb.add_argument("--per-step", type=int, default=1)
+    cs = sub.add_parser("counters")
+    cs.add_argument("csv")
+    cs.add_argument("--per-step", type=int, default=1)
     st = sub.add_parser("step-traffic")
     st.add_argument("fetch_csv")
     st.add_argument("write_csv")
@@ -219,6 +246,8 @@ def main(argv=None) -> int:
         print(json.dumps(traffic_summary(a.fetch_csv, a.write_csv, a.copy_mib, a.per_step), indent=1))
     elif a.cmd == "mfma-busy":
         print(json.dumps(mfma_busy_summary(a.csv, a.per_step), indent=1))
+    elif a.cmd == "counters":
+        print(json.dumps(counter_summary(a.csv, a.per_step), indent=1))
     else:
         print(json.dumps(step_traffic(a.fetch_csv, a.write_csv, a.copy_mib, a.calls), indent=1))
     return 0

@@ -121,3 +121,25 @@ def test_kernel_names_demangled_by_the_profiler():
     assert _short(dem) == "gemm_epilogue_kernel<256,256,64,2,2,2,6,bf16,red>"
     garbled = "void fuseml_gemm::gemm_epilogue_kernel<256, 256, 64, 2, 2, 2, 6, bool _Accum, bool, E>(fuseml_gemm_desc)"
     assert _short(garbled) == "gemm_epilogue_kernel<256,256,64,2,2,2,6,...>"
+
+
+def test_counter_summary_means_per_launch_and_wave(tmp_path):
+    """`counters` averages each counter per (kernel, launch) and per wave of the grid."""
+    from fuseml_amd.profiling import counter_summary
+
+    rows = []
+    did = 0
+    for step in range(2):
+        for pos, vals in ((0, (100.0, 4.0)), (1, (300.0, 0.0))):
+            did += 1
+            for c, v in zip(("SQ_INSTS_VALU", "SQ_LDS_BANK_CONFLICT"), vals):
+                rows.append({"Dispatch_Id": did, "Kernel_Name": GEMM, "Grid_Size": 128,
+                             "Counter_Name": c, "Counter_Value": v + step})
+    p = tmp_path / "c_counter_collection.csv"
+    _write(p, ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"], rows)
+    out = counter_summary(str(p), per_step=2)
+    assert out["counters"] == ["SQ_INSTS_VALU", "SQ_LDS_BANK_CONFLICT"]
+    k = {e["launch"]: e for e in out["kernels"]}
+    assert k[0]["counters"]["SQ_INSTS_VALU"] == 100.5 and k[1]["counters"]["SQ_INSTS_VALU"] == 300.5
+    assert k[0]["per_wave"]["SQ_INSTS_VALU"] == 50.2 or k[0]["per_wave"]["SQ_INSTS_VALU"] == 50.3
+    assert k[1]["counters"]["SQ_LDS_BANK_CONFLICT"] == 0.5 and k[0]["dispatches"] == 2
