@@ -17,7 +17,7 @@ import os
 import threading
 from typing import Optional
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_OPS = 16
 MAX_OPERANDS = 8
 MAX_EXTRA_OUT = 4
@@ -56,6 +56,12 @@ OP_CODES = {
 RED_SUM, RED_AMAX, RED_MEAN = 1, 2, 4
 RED_BITS = {"sum": RED_SUM, "amax": RED_AMAX, "mean": RED_MEAN}
 RED_SLOT = {"sum": 0, "amax": 1, "mean": 2}
+
+# Segment codes of fuseml_split_bf16x3 (2 bits per segment) and the two
+# layouts an fp32 group uses: A3 = hi | hf | lo, B3 = hi | lo | hf.
+SEG_HI, SEG_LO, SEG_HI_FINITE = 0, 1, 2
+SPLIT_A = SEG_HI | (SEG_HI_FINITE << 2) | (SEG_LO << 4)
+SPLIT_B = SEG_HI | (SEG_LO << 2) | (SEG_HI_FINITE << 4)
 
 # Error codes.
 OK, EINVAL, EUNSUPPORTED, EHIP, EDEVICE = 0, -1, -2, -3, -4

@@ -170,25 +170,28 @@ def group_eager_fn(group: Any) -> Optional[Callable[..., Any]]:
         return None
 
 
-def epilogue_passes(spec: EpilogueSpec) -> int:
+def epilogue_passes(spec: EpilogueSpec, gemm_is_addmm: bool = True) -> int:
     """Elementwise passes over the [M,N] result that eager PyTorch runs after
-    the GEMM for this group: every epilogue op except the addmm's own bias /
-    alpha / beta (hipBLASLt applies those in its GEMM epilogue) and the escape
-    stores, plus one read per reduction."""
+    the GEMM for this group: every epilogue op except the escape stores and,
+    when the group's GEMM is an ``addmm``, its own alpha / bias terms
+    (hipBLASLt applies those in its GEMM epilogue), plus one read per
+    reduction.  After an ``mm`` every op is a pass of its own: ``x @ W + b``
+    or a residual add runs as a separate eager kernel."""
     ops = list(spec.ops)
-    # the addmm's own terms come first: scale (alpha), then the bias (add of
-    # a broadcast vector or scalar)
     i = 0
-    if i < len(ops) and ops[i].kind == "scale":
-        i += 1
-    if i < len(ops) and ops[i].kind in ("add", "add_scalar"):
-        i += 1
+    if gemm_is_addmm:
+        # the addmm's own terms come first: scale (alpha), then the bias (add
+        # of a broadcast vector or scalar)
+        if i < len(ops) and ops[i].kind == "scale":
+            i += 1
+        if i < len(ops) and ops[i].kind in ("add", "add_scalar"):
+            i += 1
     passes = sum(1 for o in ops[i:] if o.kind != "store")
     return passes + len(spec.reductions)
 
 
 def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOGUE_PASS,
-                      dtype: Any = None) -> Tuple[bool, str]:
+                      dtype: Any = None, gemm_is_addmm: bool = True) -> Tuple[bool, str]:
     """The fused kernel against eager (hipBLASLt GEMM + elementwise kernels).
 
     Measured on one MI355X, each fused group against its eager ops (same box,
@@ -207,7 +210,7 @@ def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOG
     (157 TFLOP/s peak), the split product at a third of the bf16 rate."""
     if k_per_pass <= 0 or dtype == torch.float32:
         return True, "fused"
-    passes = epilogue_passes(spec)
+    passes = epilogue_passes(spec, gemm_is_addmm)
     if K <= k_per_pass * passes:
         return True, "fused"
     return False, f"K={K} with {passes} elementwise pass(es): eager's GEMM is faster (crossover K <= {k_per_pass} per pass)"
@@ -340,7 +343,8 @@ class FuseMLCompiler:
                     spec = None
                 if spec is not None:
                     K, ab_dtype = _gemm_k(group)
-                    win, why = (fused_beats_eager(spec, K, self.k_per_epilogue_pass, ab_dtype)
+                    addmm = group.base_node.target is TRIGGER_TARGETS[0]
+                    win, why = (fused_beats_eager(spec, K, self.k_per_epilogue_pass, ab_dtype, addmm)
                                 if K else (True, "fused"))
                     if not win:
                         logger.info("group %s stays eager: %s", group, why)
@@ -398,6 +402,12 @@ class FuseMLCompiler:
             if m1 is None or list(ph1.users) != [ph2]:
                 continue
             g1, g2 = ph1.meta["fusion_group"], ph2.meta["fusion_group"]
+            # both GEMMs must pass the pre-scan's cost model (tiny outputs and
+            # few-tile long-K GEMMs stay eager whichever kernel would run them)
+            verdicts = [g.base_node.meta.get("fuseml_cost_model") for g in (g1, g2)]
+            if verdicts != ["fused", "fused"]:
+                logger.info("MLP pair %s + %s stays unbound: %s", g1, g2, verdicts)
+                continue
             n1, n2 = len(g1.inputs), len(g2.inputs)
             slots1 = {k: m1[k] for k in ("x", "w1t", "b1")}
             slots2 = {k: m2[k] for k in ("h", "w2t", "b2", "r")}

@@ -50,6 +50,7 @@
 
 #include <type_traits>
 
+#include "amax_order.h"
 #include "fuseml_hip.h"
 #include "gelu_phi.h"
 #include "gemm_epilogue_shared.h"
@@ -233,19 +234,15 @@ __device__ __forceinline__ void store_out4(const Out& o, int m, int n, int M, in
   }
 }
 
-// Float atomic max through integer atomics: non-negative floats order like
-// signed ints, negative floats order inversely like unsigned ints.  A NaN is
-// written as the positive quiet NaN 0x7fc00000, which as a signed int exceeds
-// every positive float (so later signed maxima keep it) and as an unsigned int
-// is below every negative float (so later unsigned minima keep it): the
-// result is NaN once any partial is, as in torch.amax.
+// Float atomic max through integer atomics, dispatched on the sign bit
+// (amax_order.h: -0.0 takes the unsigned-min path like every other value with
+// the sign bit set; NaN is written as 0x7fc00000 and then always kept).
 __device__ __forceinline__ void atomic_max_f32(float* p, float v) {
-  if (__builtin_isnan(v))
-    atomicMax(reinterpret_cast<int*>(p), 0x7fc00000);
-  else if (v >= 0.0f)
-    atomicMax(reinterpret_cast<int*>(p), __float_as_int(v));
+  uint32_t bits;
+  if (fuseml_amax::atomic_for(__float_as_uint(v), &bits) == fuseml_amax::kSignedMax)
+    atomicMax(reinterpret_cast<int*>(p), (int)bits);
   else
-    atomicMin(reinterpret_cast<unsigned int*>(p), __float_as_uint(v));
+    atomicMin(reinterpret_cast<unsigned int*>(p), bits);
 }
 
 

@@ -11,9 +11,15 @@
 // MFMA's fp32 accumulator.  The three terms are one bf16 GEMM over a K axis
 // three times as long: row r of the split operand is three segments of k_pad
 // columns, segment s holding hi or lo parts of row r, so that
-//     A3 = [hi(A) | hi(A) | lo(A)],   B3 = [hi(B) | lo(B) | hi(B)]
+//     A3 = [hi(A) | hf(A) | lo(A)],   B3 = [hi(B) | lo(B) | hf(B)]
 // gives A3 . B3 = the three-term product, and the existing GEMM+epilogue
 // kernels run unchanged on (A3, B3, K' = 3 k_pad).
+// Non-finite values: lo(inf) = lo(NaN) = 0, and hf(x) is hi(x) with every
+// non-finite x written as 0.  Only the hi.hi segment then carries inf and
+// NaN: the cross terms hf(a) lo(b) and lo(a) hf(b) are finite, where
+// hi(inf) lo(b) would be inf * 0 = NaN for any b exact in bf16.  So a row
+// with an inf gives inf (or NaN where fp32 gives NaN: inf * 0, inf - inf),
+// as fp32 does.
 //
 // The reference runs fp32 GEMM inputs through Triton's default tf32 `tl.dot`
 // (fuseml/codegen/kernel_generator.py:1536), whose inputs keep 10 mantissa
@@ -46,20 +52,22 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
-// hi and lo parts of two values, packed as bf16 pairs.  A value whose nearest
-// bf16 would overflow (|x| above the largest finite bf16) takes the truncated
-// hi part instead, so that hi stays finite and lo carries the rest.  Inf and
-// NaN keep lo = 0: the product then is what fp32 gives (inf, or NaN).
-__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+// hi, lo and hf parts of two values, packed as bf16 pairs.  A value whose
+// nearest bf16 would overflow (|x| above the largest finite bf16) takes the
+// truncated hi part instead, so that hi stays finite and lo carries the rest.
+// Inf and NaN have lo = 0 and hf = 0 (hf is hi with non-finite values zeroed).
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo, uint32_t& hf) {
   uint32_t h = pack_bf16x2(a, b);
   const uint32_t ta = __float_as_uint(a) >> 16, tb = __float_as_uint(b) & 0xffff0000u;
-  if (__builtin_fabsf(a) > kBf16Max && __builtin_isfinite(a)) h = (h & 0xffff0000u) | ta;
-  if (__builtin_fabsf(b) > kBf16Max && __builtin_isfinite(b)) h = (h & 0x0000ffffu) | tb;
+  const bool fa = __builtin_isfinite(a), fb = __builtin_isfinite(b);
+  if (__builtin_fabsf(a) > kBf16Max && fa) h = (h & 0xffff0000u) | ta;
+  if (__builtin_fabsf(b) > kBf16Max && fb) h = (h & 0x0000ffffu) | tb;
   const float ha = __uint_as_float(h << 16), hb = __uint_as_float(h & 0xffff0000u);
-  const float ra = __builtin_isfinite(a) ? a - ha : 0.0f;
-  const float rb = __builtin_isfinite(b) ? b - hb : 0.0f;
+  const float ra = fa ? a - ha : 0.0f;
+  const float rb = fb ? b - hb : 0.0f;
   hi = h;
   lo = pack_bf16x2(ra, rb);
+  hf = h & ((fa ? 0x0000ffffu : 0u) | (fb ? 0xffff0000u : 0u));
 }
 
 // Thread t of the grid-stride loop handles row t / groups, columns
@@ -67,7 +75,7 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 template <bool kContig>
 __global__ void __launch_bounds__(kThreads)
 split_bf16x3_kernel(const float* __restrict__ src, int64_t rows, int64_t K, int64_t stride_r, int64_t stride_k,
-                    uint16_t* __restrict__ dst, int64_t ld_dst, int64_t k_pad, uint32_t lo_mask) {
+                    uint16_t* __restrict__ dst, int64_t ld_dst, int64_t k_pad, uint32_t seg_codes) {
   const int64_t groups = k_pad / 8;
   const int64_t total = rows * groups;
   for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (int64_t)gridDim.x * kThreads) {
@@ -83,19 +91,23 @@ split_bf16x3_kernel(const float* __restrict__ src, int64_t rows, int64_t K, int6
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = k0 + e < K ? src[r * stride_r + (k0 + e) * stride_k] : 0.0f;
     }
-    uint32_t hi[4], lo[4];
+    uint32_t hi[4], lo[4], hf[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) split2(x[2 * q], x[2 * q + 1], hi[q], lo[q]);
+    for (int q = 0; q < 4; ++q) split2(x[2 * q], x[2 * q + 1], hi[q], lo[q], hf[q]);
     const uint4 H = make_uint4(hi[0], hi[1], hi[2], hi[3]);
     const uint4 L = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    const uint4 HF = make_uint4(hf[0], hf[1], hf[2], hf[3]);
     uint16_t* row = dst + r * ld_dst + k0;
-    // lo_mask is uniform: a branch per segment (a select of the two vectors
+    // seg_codes is uniform: a branch per segment (a select of the vectors
     // would go through scratch memory).
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       uint4* p = reinterpret_cast<uint4*>(row + s * k_pad);
-      if ((lo_mask >> s) & 1u)
+      const uint32_t code = (seg_codes >> (2 * s)) & 3u;
+      if (code == FUSEML_SEG_LO)
         *p = L;
+      else if (code == FUSEML_SEG_HI_FINITE)
+        *p = HF;
       else
         *p = H;
     }
@@ -109,12 +121,14 @@ void set_error(const char* msg) { fuseml_detail::set_error_text(msg); }
 extern "C" {
 
 int fuseml_split_bf16x3(const float* src, int64_t rows, int64_t K, int64_t stride_r, int64_t stride_k, void* dst,
-                        int64_t ld_dst, int64_t k_pad, uint32_t lo_mask, void* stream) {
+                        int64_t ld_dst, int64_t k_pad, uint32_t seg_codes, void* stream) {
   set_error("");
-  if (rows < 0 || K < 0 || stride_r < 0 || stride_k < 0 || k_pad < K || k_pad % 8 != 0 || (lo_mask & ~7u) ||
+  bool codes_ok = (seg_codes >> 6) == 0;
+  for (int s = 0; s < 3; ++s) codes_ok = codes_ok && ((seg_codes >> (2 * s)) & 3u) <= FUSEML_SEG_HI_FINITE;
+  if (rows < 0 || K < 0 || stride_r < 0 || stride_k < 0 || k_pad < K || k_pad % 8 != 0 || !codes_ok ||
       ld_dst < 3 * k_pad || ld_dst % 8 != 0) {
     set_error("split_bf16x3: bad sizes (need 0 <= K <= k_pad, k_pad % 8 == 0, ld_dst >= 3 k_pad, ld_dst % 8 == 0, "
-              "lo_mask < 8)");
+              "three 2-bit segment codes each <= FUSEML_SEG_HI_FINITE)");
     return FUSEML_EINVAL;
   }
   if (rows == 0 || k_pad == 0) return FUSEML_OK;
@@ -134,10 +148,10 @@ int fuseml_split_bf16x3(const float* src, int64_t rows, int64_t K, int64_t strid
   uint16_t* d = reinterpret_cast<uint16_t*>(dst);
   if (contig)
     hipLaunchKernelGGL(split_bf16x3_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s, src, rows, K,
-                       stride_r, stride_k, d, ld_dst, k_pad, lo_mask);
+                       stride_r, stride_k, d, ld_dst, k_pad, seg_codes);
   else
     hipLaunchKernelGGL(split_bf16x3_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, src, rows, K,
-                       stride_r, stride_k, d, ld_dst, k_pad, lo_mask);
+                       stride_r, stride_k, d, ld_dst, k_pad, seg_codes);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     char msg[256];

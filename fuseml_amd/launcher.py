@@ -305,19 +305,20 @@ class HipKernelLauncher:
 
     def _split_operands(self, plan: _Plan, a: torch.Tensor, b: torch.Tensor, stream: int):
         """fp32 GEMM operands as bf16 split parts on the launch stream:
-        A3 [M, 3 k_pad] = [hi|hi|lo] of A, B3 [N, 3 k_pad] = [hi|lo|hi] of the
-        weight rows (B[k, n] = b[k, n]), so that A3 . B3^T is the three-term
-        product.  Both are rebuilt on every call (4 bytes read and 6 written
-        per element of each operand); caching B3 for a weight would need a
-        reliable signal that the weight is unchanged."""
+        A3 [M, 3 k_pad] = [hi|hf|lo] of A, B3 [N, 3 k_pad] = [hi|lo|hf] of the
+        weight rows (B[k, n] = b[k, n]; hf = hi with inf/NaN written as 0), so
+        that A3 . B3^T is the three-term product with inf/NaN only in hi.hi.
+        Both are rebuilt on every call (4 bytes read and 6 written per element
+        of each operand); caching B3 for a weight would need a reliable signal
+        that the weight is unchanged."""
         kp = plan.k_split
         M, N, K = plan.M, plan.N, plan.K
         a3 = torch.empty((M, 3 * kp), dtype=torch.bfloat16, device=a.device)
         b3 = torch.empty((N, 3 * kp), dtype=torch.bfloat16, device=b.device)
-        for src, rows, sr, sk, dst, mask in ((a, M, a.stride(0), a.stride(1), a3, 0b100),
-                                             (b, N, b.stride(1), b.stride(0), b3, 0b010)):
+        for src, rows, sr, sk, dst, codes in ((a, M, a.stride(0), a.stride(1), a3, _abi.SPLIT_A),
+                                              (b, N, b.stride(1), b.stride(0), b3, _abi.SPLIT_B)):
             rc = self._lib.fuseml_split_bf16x3(ctypes.c_void_p(src.data_ptr()), rows, K, sr, sk,
-                                               ctypes.c_void_p(dst.data_ptr()), 3 * kp, kp, mask,
+                                               ctypes.c_void_p(dst.data_ptr()), 3 * kp, kp, codes,
                                                ctypes.c_void_p(stream))
             if rc != _abi.OK:
                 raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FUSEML_ABI_VERSION 3
+#define FUSEML_ABI_VERSION 4
 
 #define FUSEML_MAX_OPS 16
 #define FUSEML_MAX_OPERANDS 8
@@ -223,15 +223,26 @@ int fuseml_mlp_block_supported(const fuseml_mlp_desc* desc);
  *
  * src element (r,k) is src[r*stride_r + k*stride_k], r < rows, k < K (any
  * non-negative strides).  Row r of dst (bf16, row stride ld_dst) is three
- * segments of k_pad columns; segment s holds lo(x) = bf16(x - bf16(x)) if
- * bit s of lo_mask is set, else hi(x) = bf16(x); columns K..k_pad-1 are 0.
- * With A3 from lo_mask 4 (hi|hi|lo) and B3 from lo_mask 2 (hi|lo|hi),
- * A3 . B3 = hi.hi + hi.lo + lo.hi.  Needs k_pad % 8 == 0, k_pad >= K,
- * ld_dst % 8 == 0, ld_dst >= 3 k_pad and a 16-byte aligned dst.
+ * segments of k_pad columns; segment s holds the part named by the 2-bit code
+ * (seg_codes >> 2s) & 3:
+ *   FUSEML_SEG_HI        hi(x) = bf16(x) (round to nearest even; the truncated
+ *                        bits where that would overflow a finite x),
+ *   FUSEML_SEG_LO        lo(x) = bf16(x - hi(x)), 0 for inf and NaN,
+ *   FUSEML_SEG_HI_FINITE hi(x), with 0 for inf and NaN;
+ * columns K..k_pad-1 are 0.  With A3 from FUSEML_SPLIT_A (hi|hf|lo) and B3
+ * from FUSEML_SPLIT_B (hi|lo|hf), A3 . B3 = hi.hi + hf.lo + lo.hf: the cross
+ * terms are finite, so inf and NaN reach the product only through hi.hi, as
+ * fp32 gives them.  Needs k_pad % 8 == 0, k_pad >= K, ld_dst % 8 == 0,
+ * ld_dst >= 3 k_pad and a 16-byte aligned dst.
  * Asynchronous on `stream`; 0 or a FUSEML_E* code.
  * ------------------------------------------------------------------------ */
+#define FUSEML_SEG_HI 0u
+#define FUSEML_SEG_LO 1u
+#define FUSEML_SEG_HI_FINITE 2u
+#define FUSEML_SPLIT_A (FUSEML_SEG_HI | (FUSEML_SEG_HI_FINITE << 2) | (FUSEML_SEG_LO << 4))
+#define FUSEML_SPLIT_B (FUSEML_SEG_HI | (FUSEML_SEG_LO << 2) | (FUSEML_SEG_HI_FINITE << 4))
 int fuseml_split_bf16x3(const float* src, int64_t rows, int64_t K, int64_t stride_r, int64_t stride_k, void* dst,
-                        int64_t ld_dst, int64_t k_pad, uint32_t lo_mask, void* stream);
+                        int64_t ld_dst, int64_t k_pad, uint32_t seg_codes, void* stream);
 
 /* Measurement only (no reference counterpart; the reference's benchmark
  * prices against a spec table, benchmarks/bench_mlp_block.py:228-412): launch

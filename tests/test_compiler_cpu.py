@@ -243,6 +243,43 @@ def test_epilogue_passes_and_crossover_rule():
     assert not fused_beats_eager(g2, 4096)[0] and not fused_beats_eager(g1, 4096)[0]
     assert not fused_beats_eager(g2, 16384)[0]
     assert fused_beats_eager(g2, 16384, k_per_pass=0)[0]
+    # After an mm (no addmm bias) a leading add is an eager pass of its own.
+    mm_add = EpilogueSpec(0, 1, (EpiOp("add", 2),), BF)
+    mm_add_gelu = EpilogueSpec(0, 1, (EpiOp("add", 2), EpiOp("gelu_erf")), BF)
+    assert epilogue_passes(mm_add, gemm_is_addmm=False) == 1
+    assert epilogue_passes(mm_add, gemm_is_addmm=True) == 0
+    assert epilogue_passes(mm_add_gelu, gemm_is_addmm=False) == 2
+    assert fused_beats_eager(mm_add, 1024, gemm_is_addmm=False)[0]
+    assert fused_beats_eager(mm_add_gelu, 2048, gemm_is_addmm=False)[0]
+    assert not fused_beats_eager(mm_add_gelu, 2048, gemm_is_addmm=True)[0]
+
+
+class _MmAddGelu(nn.Module):
+    """gelu(x @ W.T + b) written without F.linear: the graph is mm -> add ->
+    gelu, two eager passes after the GEMM."""
+
+    def __init__(self, d_in, d_out):
+        super().__init__()
+        self.w = nn.Parameter(torch.randn(d_out, d_in) / d_in ** 0.5)
+        self.b = nn.Parameter(torch.randn(d_out) * 0.1)
+
+    def forward(self, x):
+        return F.gelu(x @ self.w.t() + self.b)
+
+
+def test_mm_add_counts_the_add_as_a_pass(recorded):
+    """K = 2048 with two passes (add, gelu) is inside the measured crossover
+    (K <= 1024 x passes), so the mm-based group fuses; counted as an addmm's
+    free bias it would have one pass and stay eager."""
+    torch.manual_seed(0)
+    m = _MmAddGelu(2048, 256).to(BF).eval()
+    x = torch.randn(64, 2048, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0, min_tiles_long_k=0)
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+    assert torch.allclose(out.float(), m(x).float(), atol=2e-2)
+    assert [s.spec.describe() for s in recorded.built] == ["gemm(0,1) -> add[2] -> gelu_erf"]
+    assert be.fusion_strategy == "hip"
 
 
 def test_long_k_groups_route_to_eager(recorded):

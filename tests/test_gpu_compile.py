@@ -67,6 +67,47 @@ def test_few_tiles_long_k_is_routed_to_eager():
     _close(out, _f64(ref), "fused Linear+GELU")
 
 
+class _NegReluAmax(torch.nn.Module):
+    def __init__(self, w):
+        super().__init__()
+        self.w = torch.nn.Parameter(w, requires_grad=False)
+
+    def forward(self, x):
+        return (torch.relu(x @ self.w.t()) * -1).amax(-1)
+
+
+def test_compiled_amax_of_negated_relu():
+    """(relu(x @ W.T) * -1).amax(-1) under the default cost model: default
+    discovery forms one group mm -> relu -> mul(-1) -> amax (three eager
+    passes at K = 1024, so it fuses).  Every value is <= 0 and relu's +0
+    becomes -0.0, so each row maximum is -0.0 (row 7 of x is zero: that whole
+    row is -0.0); the fused amax must return -0.0 there, not -inf or the
+    largest strictly negative value."""
+    from fuseml_amd.compiler import FuseMLCompiler
+
+    gen = torch.Generator().manual_seed(71)
+    x = torch.randn(1024, 1024, generator=gen).to(torch.bfloat16)
+    x[7] = 0
+    w = (torch.randn(2048, 1024, generator=gen) / 32).to(torch.bfloat16)
+    m = _NegReluAmax(w).to("cuda")
+    xd = x.to("cuda")
+    torch._dynamo.reset()
+    be = FuseMLCompiler()
+    compiled = torch.compile(m, backend=be)
+    with torch.no_grad():
+        got = compiled(xd)
+        eager = m(xd)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and len(be.launchers) == 1 and _launches(be) == 1
+    assert be.launchers[0].spec.reductions == ("amax",)
+    ref = (-np.maximum(_f64(x) @ _f64(w).T, 0.0)).max(axis=1)
+    g = _f64(got)
+    assert np.isfinite(g).all(), f"rows with -inf: {np.argwhere(~np.isfinite(g)).ravel()[:8]}"
+    assert np.allclose(g, ref, rtol=2e-2, atol=2e-2)
+    assert torch.equal(got.float(), eager.float())
+    assert g[7] == 0.0 and np.signbit(g[7])
+
+
 def test_c1_fp32_small_is_bypassed():
     from fuseml_amd.workloads import c1_transformer_mlp_small
 

@@ -241,6 +241,42 @@ def test_variant_reductions_parity(forced_variant, axis):
 
 @pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
 @pytest.mark.parametrize("axis", [1, 0])
+@pytest.mark.parametrize("shape", [(600, 1030, 200), (257, 512, 72), (64, 96, 40)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_variant_amax_of_nonpositive_values(forced_variant, axis, shape):
+    """relu -> scale(-1) -> amax: every value is <= 0, and relu's +0 becomes
+    -0.0, so most maxima are -0.0.  The fp32 atomic max must fold a -0.0
+    partial in (it has the sign bit set: the unsigned-min path); one row of A
+    and one row of W are all zero, so a whole output row and a whole column
+    hold nothing but -0.0, whose maximum is -0.0, not the -inf fill."""
+    M, N, K = shape
+    K = _k_for(forced_variant, K)
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=61)
+    a[min(3, M - 1)] = 0
+    w[min(5, N - 1)] = 0
+    steps = [("relu", -1, 1.0), ("scale", -1, -1.0)]
+    spec = _spec(left=0, right=1, ops=steps, out_dtype=dtype, store_tile=True,
+                 reductions=("amax", "sum"), reduce_axis=axis,
+                 reduce_dtypes=(torch.float32,) * 2,
+                 outputs=(("tile",), ("red", "amax"), ("red", "sum")))
+    print(f"case variant={forced_variant} nonpositive amax axis={axis} shape={shape}", flush=True)
+    tile, mx, s = _launcher(spec, 2)(a.cuda(), w.t().cuda())
+    torch.cuda.synchronize()
+    ref = ora.gemm_epilogue([_np(a), _np(w.t())], 0, 1, steps, ("amax", "sum"), axis)
+    v = ref["tile"]
+    assert (v <= 0).all()
+    _check_tile(tile, v, f"{forced_variant} tile")
+    got = _np(mx)
+    assert np.isfinite(got).all(), f"amax has -inf: {np.argwhere(~np.isfinite(got))[:5].ravel()}"
+    _check_red(mx, ref["amax"], np.abs(v).max(axis=axis), "amax")
+    _check_red(s, ref["sum"], np.abs(v).sum(axis=axis), "sum")
+    zero_line = min(3, M - 1) if axis == 1 else min(5, N - 1)
+    assert got[zero_line] == 0.0 and np.signbit(got[zero_line]), "all -0.0 line must give -0.0"
+
+
+@pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
+@pytest.mark.parametrize("axis", [1, 0])
 @pytest.mark.parametrize("store_tile", [True, False], ids=["tile", "notile"])
 @pytest.mark.parametrize("shape", [(600, 1024, 200), (257, 512, 72)], ids=lambda s: "x".join(map(str, s)))
 def test_variant_reductions_with_tile_operand(forced_variant, axis, store_tile, shape):
@@ -517,7 +553,7 @@ def _split_bits_ref(x: torch.Tensor):
     return hi, lo
 
 
-def _split_on_device(x: torch.Tensor, lo_mask: int):
+def _split_on_device(x: torch.Tensor, seg_codes: int):
     from fuseml_amd import _abi
 
     lib = _abi.load_library()
@@ -525,15 +561,20 @@ def _split_on_device(x: torch.Tensor, lo_mask: int):
     kp = -(-K // 8) * 8
     dst = torch.full((rows, 3 * kp), 0x7777, dtype=torch.int16, device=x.device)
     rc = lib.fuseml_split_bf16x3(x.data_ptr(), rows, K, x.stride(0), x.stride(1), dst.data_ptr(), 3 * kp, kp,
-                                 lo_mask, torch.cuda.current_stream().cuda_stream)
+                                 seg_codes, torch.cuda.current_stream().cuda_stream)
     assert rc == 0, _abi.last_error(lib)
     torch.cuda.synchronize()
     return dst.cpu(), kp
 
 
 @pytest.mark.parametrize("layout", ["contig", "ragged_k", "strided_k", "transposed", "one_row"])
-@pytest.mark.parametrize("lo_mask", [0b100, 0b010])
-def test_split_bf16x3_bit_exact(layout, lo_mask):
+@pytest.mark.parametrize("seg_codes", ["A", "B"])
+def test_split_bf16x3_bit_exact(layout, seg_codes):
+    """Segment s of each row holds hi, lo or hf (hi with inf/NaN written as 0)
+    as the 2-bit code says: A3 = hi|hf|lo, B3 = hi|lo|hf."""
+    from fuseml_amd import _abi
+
+    codes = {"A": _abi.SPLIT_A, "B": _abi.SPLIT_B}[seg_codes]
     g = _gen(60)
     shapes = {"contig": (300, 64), "ragged_k": (37, 100), "strided_k": (41, 3 * 77), "transposed": (56, 33),
               "one_row": (1, 24)}
@@ -543,15 +584,19 @@ def test_split_bf16x3_bit_exact(layout, lo_mask):
                 3.4028235e38, 3.3895314e38, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -9]
     base.view(-1)[: len(specials)] = torch.tensor(specials)
     x = {"strided_k": lambda t: t[:, ::3], "transposed": lambda t: t.t()}.get(layout, lambda t: t)(base)
-    print(f"case split layout={layout} mask={lo_mask} shape={tuple(x.shape)} stride={x.stride()}", flush=True)
-    got, kp = _split_on_device(x.cuda(), lo_mask)
+    print(f"case split layout={layout} codes={seg_codes} shape={tuple(x.shape)} stride={x.stride()}", flush=True)
+    got, kp = _split_on_device(x.cuda(), codes)
     hi, lo = _split_bits_ref(x)
     K = x.shape[1]
     nan = torch.isnan(x)
+    fin = torch.isfinite(x)
     for seg in range(3):
         part = got[:, seg * kp: seg * kp + K]
-        if (lo_mask >> seg) & 1:
+        code = (codes >> (2 * seg)) & 3
+        if code == _abi.SEG_LO:
             ok = part == lo                                   # lo of inf/NaN is 0
+        elif code == _abi.SEG_HI_FINITE:
+            ok = torch.where(fin, part == hi, part == 0)      # hf of inf/NaN is 0
         else:
             as_f = (part.to(torch.int32) << 16).view(torch.float32)
             ok = torch.where(nan, torch.isnan(as_f), part == hi)
@@ -594,6 +639,45 @@ def test_fp32_graph_capture_replays():
         assert torch.equal(g_out, eager), f"replay seed {seed} differs from eager"
         ref = ora.gemm_epilogue([_np(t) for t in host], 1, 2, [("add", 0, 1.0), ("gelu_erf", -1, 1.0)])["tile"]
         assert np.isclose(_np(g_out), ref, rtol=FP32_RTOL, atol=FP32_ATOL).all()
+
+
+@pytest.mark.parametrize("shape", [(77, 200, 72), (300, 520, 13)], ids=lambda s: "x".join(map(str, s)))
+def test_fp32_group_with_inf_and_nan_operands(shape):
+    """Non-finite fp32 GEMM operands give what fp32 gives: +-inf in A and in W
+    next to values exact in bf16 (lo = 0, so hi(inf) . lo(b) would be
+    inf * 0 = NaN), a NaN in each.  The NaN / +inf / -inf pattern of the fused
+    result equals torch fp32's on the CPU exactly (it depends only on which
+    products are infinite, not on the summation order); finite values agree
+    to 1e-4."""
+    M, N, K = shape
+    a, w = _gemm_inputs(M, N, K, torch.float32, seed=81)
+    # exact in bf16, so their lo part is 0; no exact zeros (0 * inf is NaN in
+    # fp32, and a reference that skipped zero products would hide it)
+    a[:, ::2] = torch.round(a[:, ::2] * 4) / 4
+    a[a == 0] = 0.5
+    w[::2, :] = torch.round(w[::2, :] * 8) / 8
+    w[w == 0] = -0.125
+    a[0, 1] = float("inf")
+    a[3, K - 1] = -float("inf")
+    a[5, 0] = float("nan")
+    w[2, 3 % K] = float("inf")
+    w[7, 5 % K] = -float("inf")
+    w[11, (K - 2) % K] = float("nan")
+    bias = torch.rand(N, generator=_gen(82)) - 0.5
+    steps = [("add", 0, 1.0), ("relu", -1, 1.0)]
+    spec = _spec(left=1, right=2, ops=steps, out_dtype=torch.float32)
+    print(f"case fp32 inf/nan operands shape={shape}", flush=True)
+    out = _launcher(spec, 3)(bias.cuda(), a.cuda(), w.t().cuda())
+    torch.cuda.synchronize()
+    ref = torch.relu(torch.addmm(bias, a, w.t()))      # torch fp32 on the CPU
+    got = out.cpu()
+    for what, mask in (("nan", torch.isnan), ("+inf", lambda t: t == float("inf")),
+                       ("-inf", lambda t: t == -float("inf"))):
+        g, r = mask(got), mask(ref)
+        assert torch.equal(g, r), f"{what}: {int((g != r).sum())} positions differ, e.g. {torch.nonzero(g != r)[:4].tolist()}"
+    assert int(torch.isinf(ref).sum()) > 0 and int(torch.isnan(ref).sum()) > 0
+    fin = torch.isfinite(ref)
+    assert torch.allclose(got[fin], ref[fin], rtol=FP32_RTOL, atol=FP32_ATOL)
 
 
 FP32_CHAINS = ["bias_gelu", "act_heavy", "scalars", "bcast_mul", "bias_residual", "sigmoid"]

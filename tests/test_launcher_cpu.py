@@ -42,9 +42,9 @@ class Recorder:
         self.calls.append(snap)
         return self.rc
 
-    def fuseml_split_bf16x3(self, src, rows, K, stride_r, stride_k, dst, ld_dst, k_pad, lo_mask, stream):
+    def fuseml_split_bf16x3(self, src, rows, K, stride_r, stride_k, dst, ld_dst, k_pad, seg_codes, stream):
         self.splits.append({"src": src.value, "rows": rows, "K": K, "sr": stride_r, "sk": stride_k,
-                            "dst": dst.value, "ld": ld_dst, "k_pad": k_pad, "mask": lo_mask})
+                            "dst": dst.value, "ld": ld_dst, "k_pad": k_pad, "mask": seg_codes})
         return self.split_rc
 
     def fuseml_last_error(self):
@@ -197,8 +197,8 @@ def test_fp32_operands_are_split_then_one_bf16_gemm():
     b, x, w = torch.randn(N), torch.randn(M, K), torch.randn(N, K)
     out = make(spec, 3, rec)(b, x, w.t())
     sa, sb = rec.splits
-    assert (sa["src"], sa["rows"], sa["K"], sa["sr"], sa["sk"], sa["mask"]) == (x.data_ptr(), M, K, K, 1, 0b100)
-    assert (sb["src"], sb["rows"], sb["K"], sb["sr"], sb["sk"], sb["mask"]) == (w.data_ptr(), N, K, K, 1, 0b010)
+    assert (sa["src"], sa["rows"], sa["K"], sa["sr"], sa["sk"], sa["mask"]) == (x.data_ptr(), M, K, K, 1, _abi.SPLIT_A)
+    assert (sb["src"], sb["rows"], sb["K"], sb["sr"], sb["sk"], sb["mask"]) == (w.data_ptr(), N, K, K, 1, _abi.SPLIT_B)
     assert sa["k_pad"] == sb["k_pad"] == 16 and sa["ld"] == sb["ld"] == 48
     c = rec.calls[0]
     assert (c["M"], c["N"], c["K"], c["lda"], c["ldb"], c["ab"]) == (M, N, 48, 48, 48, _abi.BF16)

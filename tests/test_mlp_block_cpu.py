@@ -79,6 +79,21 @@ def test_unsupported_width_keeps_two_launches(monkeypatch):
     assert len(be.launchers) == 2
 
 
+def test_pair_with_a_tiny_second_gemm_keeps_two_launches(monkeypatch):
+    """x[256,256] -> 4096 -> 256: the first GEMM's output (1M elements) passes
+    the tiny-output rule, the second's (65k) does not, so the pair is not bound
+    to the single-kernel MLP: the first group fuses and the second runs eager."""
+    torch.manual_seed(0)
+    m = TransformerMLP(256, 4096).to(BF).eval()
+    x = torch.randn(256, 256, dtype=BF)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    be = FuseMLCompiler(require_gfx950=False, fuse_mlp_block=True)
+    with torch.no_grad():
+        assert torch.equal(_compile(m, be)(x), m(x))
+    assert not any(isinstance(l, HipMlpLauncher) for l in be.launchers)
+    assert len(be.launchers) == 1 and be.fusion_strategy == "mixed"
+
+
 class _Recorder:
     def __init__(self):
         self.calls = []
