@@ -74,6 +74,7 @@ EXPORTED_SYMBOLS = (
     "fuseml_gemm_epilogue_supported",
     "fuseml_gemm_epilogue_config",
     "fuseml_gemm_epilogue_force_variant",
+    "fuseml_gemm_epilogue_chain",
     "fuseml_last_error",
     "fuseml_device_arch",
     "fuseml_abi_version",
@@ -188,6 +189,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fuseml_gemm_epilogue_config.restype = ctypes.c_int
     lib.fuseml_gemm_epilogue_force_variant.argtypes = [ctypes.c_char_p]
     lib.fuseml_gemm_epilogue_force_variant.restype = ctypes.c_int
+    lib.fuseml_gemm_epilogue_chain.argtypes = [desc_p]
+    lib.fuseml_gemm_epilogue_chain.restype = ctypes.c_int
     lib.fuseml_last_error.argtypes = []
     lib.fuseml_last_error.restype = ctypes.c_char_p
     lib.fuseml_device_arch.argtypes = [ctypes.c_int, ctypes.c_char_p, ctypes.c_int]

@@ -59,15 +59,18 @@ constexpr int64_t kTileSpan = 256;  // largest tile edge of any variant
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Pinned variant: 0 automatic, else 1 + index into {large, deep, deep3, small}.
-// Initialised once per process from FUSEML_HIP_TILE, changed only through
-// fuseml_gemm_epilogue_force_variant.
-constexpr const char* kVariantNames[] = {"large", "deep", "deep3", "small"};
+// Pinned variant: 0 automatic, else 1 + index into {large, deep, deep3, small,
+// deep3-generic} (the last: deep3 with the generic op loop even where a fixed
+// chain matches).  Initialised once per process from FUSEML_HIP_TILE, changed
+// only through fuseml_gemm_epilogue_force_variant.
+constexpr const char* kVariantNames[] = {"large", "deep", "deep3", "small", "deep3-generic"};
+constexpr int kNumVariantNames = 5;
+constexpr int kForcedDeep3Generic = 5;
 std::atomic<int> g_forced_variant{-1};  // -1: environment not read yet
 
 int variant_code(const char* name) {
   if (name == nullptr || name[0] == '\0' || !strcmp(name, "auto")) return 0;
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kNumVariantNames; ++i)
     if (!strcmp(name, kVariantNames[i])) return i + 1;
   return -1;
 }
@@ -92,6 +95,7 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
     case 2: return kDeep;
     case 3: return d.K % 64 == 0 ? kDeep3 : kDeep;
     case 4: return kSmall;
+    case kForcedDeep3Generic: return d.K % 64 == 0 ? kDeep3 : kDeep;
     default: break;
   }
   // A 256x256 tile keeps the LDS traffic per MFMA low enough for the MFMA pipe
@@ -276,6 +280,48 @@ void derive_flags(fuseml_gemm_desc& d) {
   for (int i = 0; i < d.n_extra; ++i) out_flags(d.extra[i]);
 }
 
+// The fixed chain (FixedChain) that expresses the descriptor's epilogue, or
+// kChainGeneric.  Called after derive_flags: a "row" operand is a [N] vector
+// holding an LDS slot, a "tile" operand the LDS-staged bf16 2-D operand.
+// Fixed chains are built for bf16 GEMM operands, no escape stores, and no
+// reductions except after a lone relu (the ReLU + row/column reductions
+// group).
+int match_fixed_chain(const fuseml_gemm_desc& d) {
+  if (d.ab_dtype != FUSEML_BF16 || d.n_extra != 0) return kChainGeneric;
+  auto is = [&](int o, int kind) { return o < d.n_ops && d.ops[o].kind == kind; };
+  auto row = [&](int o) {
+    if (!is(o, FUSEML_OP_ADD)) return false;
+    const fuseml_operand& op = d.operands[d.ops[o].operand];
+    return (op.reserved & kFlagAux) != 0 && op.stride_m == 0;
+  };
+  auto tile = [&](int o, int kind) {
+    if (!is(o, kind)) return false;
+    const fuseml_operand& op = d.operands[d.ops[o].operand];
+    return (op.reserved & kFlagStage) != 0 && op.dtype == FUSEML_BF16;
+  };
+  int ch = kChainGeneric;
+  switch (d.n_ops) {
+    case 0: ch = kChainNone; break;
+    case 1:
+      if (row(0)) ch = kChainBias;
+      else if (is(0, FUSEML_OP_RELU)) ch = kChainRelu;
+      break;
+    case 2:
+      if (row(0) && is(1, FUSEML_OP_GELU_ERF)) ch = kChainBiasGeluErf;
+      else if (row(0) && is(1, FUSEML_OP_GELU_TANH)) ch = kChainBiasGeluTanh;
+      else if (row(0) && is(1, FUSEML_OP_RELU)) ch = kChainBiasRelu;
+      else if (row(0) && tile(1, FUSEML_OP_ADD)) ch = kChainBiasTile;
+      break;
+    case 5:
+      if (row(0) && is(1, FUSEML_OP_RELU) && tile(2, FUSEML_OP_MUL) && is(3, FUSEML_OP_SIGMOID) && row(4))
+        ch = kChainActHeavy;
+      break;
+    default: break;
+  }
+  if (d.reduce_mask != 0 && ch != kChainRelu) return kChainGeneric;
+  return ch;
+}
+
 // `max_wg` caps the grid (0: one workgroup per tile); the kernel loops over the
 // remaining tiles.
 template <const TileConfig& C>
@@ -284,19 +330,61 @@ hipError_t launch_variant(const fuseml_gemm_desc& d, hipStream_t stream, int max
   if (max_wg > 0 && tiles > max_wg) tiles = max_wg;
   const dim3 grid((unsigned)tiles), block(C.wm * C.wn * 64);
   const bool red = d.reduce_mask != 0;
+  constexpr int G = kChainGeneric;
   if (d.ab_dtype == FUSEML_BF16 && !red)
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16, false>), grid,
-                       block, 0, stream, d);
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16, false, G>),
+                       grid, block, 0, stream, d);
   else if (d.ab_dtype == FUSEML_BF16)
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16, true>), grid,
-                       block, 0, stream, d);
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16, true, G>),
+                       grid, block, 0, stream, d);
   else if (!red)
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, _Float16, false>),
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, _Float16, false, G>),
                        grid, block, 0, stream, d);
   else
-    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, _Float16, true>),
+    hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, _Float16, true, G>),
                        grid, block, 0, stream, d);
   return hipGetLastError();
+}
+
+// A fixed-chain kernel of variant C (bf16 operands; reductions only with
+// kChainRelu, as match_fixed_chain guarantees).
+template <const TileConfig& C, int CH>
+void launch_fixed_one(const fuseml_gemm_desc& d, hipStream_t stream, dim3 grid, dim3 block) {
+  if constexpr (CH == kChainRelu) {
+    if (d.reduce_mask != 0) {
+      hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16, true, CH>),
+                         grid, block, 0, stream, d);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, C.sched, __bf16, false, CH>),
+                     grid, block, 0, stream, d);
+}
+
+template <const TileConfig& C>
+hipError_t launch_fixed(const fuseml_gemm_desc& d, int ch, hipStream_t stream, int max_wg) {
+  int64_t tiles = cdiv(d.M, C.bm) * cdiv(d.N, C.bn);
+  if (max_wg > 0 && tiles > max_wg) tiles = max_wg;
+  const dim3 grid((unsigned)tiles), block(C.wm * C.wn * 64);
+  switch (ch) {
+    case kChainNone: launch_fixed_one<C, kChainNone>(d, stream, grid, block); break;
+    case kChainBias: launch_fixed_one<C, kChainBias>(d, stream, grid, block); break;
+    case kChainBiasGeluErf: launch_fixed_one<C, kChainBiasGeluErf>(d, stream, grid, block); break;
+    case kChainBiasGeluTanh: launch_fixed_one<C, kChainBiasGeluTanh>(d, stream, grid, block); break;
+    case kChainBiasRelu: launch_fixed_one<C, kChainBiasRelu>(d, stream, grid, block); break;
+    case kChainBiasTile: launch_fixed_one<C, kChainBiasTile>(d, stream, grid, block); break;
+    case kChainActHeavy: launch_fixed_one<C, kChainActHeavy>(d, stream, grid, block); break;
+    case kChainRelu: launch_fixed_one<C, kChainRelu>(d, stream, grid, block); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// The fixed chain a launch of `d` (flags derived) on variant `c` runs, or
+// kChainGeneric: fixed chains are built for the one-wave whole-stage variant.
+int launch_chain(const fuseml_gemm_desc& d, const TileConfig& c) {
+  if (c.sched != kDeep3.sched || forced_variant() == kForcedDeep3Generic) return kChainGeneric;
+  return match_fixed_chain(d);
 }
 
 // Per-device check and CU count, queried once per device: the CU count for a
@@ -368,11 +456,26 @@ int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]) {
   return FUSEML_OK;
 }
 
+int fuseml_gemm_epilogue_chain(const fuseml_gemm_desc* desc) {
+  g_last_error[0] = '\0';
+  const int rc = validate(desc);
+  if (rc != FUSEML_OK) return rc;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) {
+    const int known = g_device_cus[dev].load(std::memory_order_relaxed);
+    if (known > 0) cus = known;
+  }
+  fuseml_gemm_desc d = *desc;
+  fold_final_store(d);
+  derive_flags(d);
+  return launch_chain(d, choose_config(d, cus));
+}
+
 int fuseml_gemm_epilogue_force_variant(const char* name) {
   g_last_error[0] = '\0';
   const int v = variant_code(name);
   if (v < 0) {
-    set_error("unknown variant '%s' (large, deep, deep3, small or auto)", name);
+    set_error("unknown variant '%s' (large, deep, deep3, small, deep3-generic or auto)", name);
     return FUSEML_EINVAL;
   }
   forced_variant();  // the environment is read first, so it cannot override this later
@@ -428,7 +531,10 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
   }
 
   const TileConfig c = choose_config(d, cus);
-  if (c.sched == kDeep.sched)
+  const int ch = launch_chain(d, c);
+  if (ch != kChainGeneric)
+    e = launch_fixed<kDeep3>(d, ch, stream, cus);
+  else if (c.sched == kDeep.sched)
     e = launch_variant<kDeep>(d, stream, cus);
   else if (c.sched == kLarge.sched)
     e = launch_variant<kLarge>(d, stream, cus);

@@ -408,8 +408,12 @@ __device__ __forceinline__ i32x4_t swap_halves(i32x4_t x) { return i32x4_t{x.z, 
 // whole stage of fragments in registers (described at its loop).  RED: the
 // launch has reductions.  Only that instantiation carries the reductions' code
 // (the row partials of interior tiles as an unmasked tree); without it, a
-// staged output's block tail is the staging writes alone.
-template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T, bool RED>
+// staged output's block tail is the staging writes alone.  CH: the epilogue
+// chain (FixedChain): kChainGeneric interprets the descriptor's ops; a fixed
+// chain is the same arithmetic compiled as straight-line code (bitwise the
+// same results), which at one wave per SIMD removes the op loop's per-op
+// descriptor loads, dispatch and register copies from every column block.
+template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T, bool RED, int CH>
 __global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(SCHED >= 3 ? 1 : 2)))
 void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
   using G = StageGeom<BK>;
@@ -1151,10 +1155,101 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     });
     float* red_sum = reinterpret_cast<float*>(smem);
     float* red_max = red_sum + (d.reduce_axis == 1 ? WN * BM : WM * BN);
+    // Fixed chains: the operands' LDS slots and the ADD alphas, read once per
+    // tile (the host matched the op kinds and operand kinds to CH).  Op 0 is
+    // the row-vector ADD of every chain that has one; the act-heavy chain's
+    // second row vector is op 4, and the tile ADD of bias + tile is op 1.
+    constexpr bool kFxRow0 = CH == kChainBias || CH == kChainBiasGeluErf || CH == kChainBiasGeluTanh ||
+                             CH == kChainBiasRelu || CH == kChainBiasTile || CH == kChainActHeavy;
+    int fx_slot0 = 0, fx_slot1 = 0;
+    float fx_a0 = 1.0f, fx_a1 = 1.0f;
+    if constexpr (kFxRow0) {
+      fx_slot0 = (d.operands[d.ops[0].operand].reserved >> 8) & (kAuxSlots - 1);
+      fx_a0 = d.ops[0].scalar;
+    }
+    if constexpr (CH == kChainBiasTile) fx_a1 = d.ops[1].scalar;
+    if constexpr (CH == kChainActHeavy) {
+      fx_slot1 = (d.operands[d.ops[4].operand].reserved >> 8) & (kAuxSlots - 1);
+      fx_a1 = d.ops[4].scalar;
+    }
+    // A fixed chain over one column block (NJ row blocks x 16 values).  Every
+    // op is the generic loop's arithmetic on the same values in the same order;
+    // activations step across 16 independent values instead of 8.
+    auto fixed_ops = [&](f32x16_t(&A)[NJ], const int i) {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int l32 = ln & 31;
+      const int khalf = ln >> 5;
+      const int cb = wn * TN + 32 * i + 4 * khalf;  // this lane's first column of block i in the tile
+      auto add_row = [&](int slot, float a) {
+        const float* av = aux + slot * AUXLEN + cb;
+        float x[16];
+        static_for<0, 4>([&](auto g) {
+          const float4 q = *reinterpret_cast<const float4*>(av + 8 * g);
+          x[4 * g + 0] = q.x;
+          x[4 * g + 1] = q.y;
+          x[4 * g + 2] = q.z;
+          x[4 * g + 3] = q.w;
+        });
+        static_for<0, NJ>([&](auto j) {
+          static_for<0, 16>([&](auto r) { A[j][(int)r] = fmaf(a, x[r], A[j][(int)r]); });
+        });
+      };
+      // The staged bf16 tile's values of this block, all row blocks' 8-byte
+      // units read before any is used (32 registers).
+      auto read_tile = [&](uint2(&wb)[NJ][4]) {
+        const int u0 = (wn * TN + 32 * i) / 4 + khalf;
+        static_for<0, NJ>([&](auto j) {
+          const int r_loc = wm * TM + 32 * j + l32;
+          static_for<0, 4>([&](auto g) {
+            wb[j][g] = *reinterpret_cast<const uint2*>(stg + stage_unit<BN>(r_loc, u0 + 2 * g));
+          });
+        });
+      };
+      auto tile_value = [&](const uint2(&wb)[NJ][4], auto j, auto r) {
+        const uint32_t w = (r & 2) ? wb[j][r / 4].y : wb[j][r / 4].x;
+        return (r & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+      };
+      auto relu_all = [&]() {
+        static_for<0, NJ>([&](auto j) {
+          static_for<0, 16>([&](auto r) { A[j][(int)r] = max_nan(A[j][(int)r], 0.0f); });
+        });
+      };
+      auto activation = [&](auto fn) {
+        static_for<0, NJ>([&](auto j) {
+          float v[16];
+          static_for<0, 16>([&](auto r) { v[r] = A[j][(int)r]; });
+          fn(v);
+          static_for<0, 16>([&](auto r) { A[j][(int)r] = v[r]; });
+        });
+      };
+      if constexpr (kFxRow0) add_row(fx_slot0, fx_a0);
+      if constexpr (CH == kChainBiasGeluErf) activation([](float* v) { gelu_erf_n<16>(v); });
+      if constexpr (CH == kChainBiasGeluTanh) activation([](float* v) { gelu_tanh_n<16>(v); });
+      if constexpr (CH == kChainBiasRelu || CH == kChainRelu || CH == kChainActHeavy) relu_all();
+      if constexpr (CH == kChainBiasTile || CH == kChainActHeavy) {
+        uint2 wb[NJ][4];
+        read_tile(wb);
+        static_for<0, NJ>([&](auto j) {
+          static_for<0, 16>([&](auto r) {
+            const float x = tile_value(wb, j, r);
+            if constexpr (CH == kChainBiasTile)
+              A[j][(int)r] = fmaf(fx_a1, x, A[j][(int)r]);
+            else
+              A[j][(int)r] = A[j][(int)r] * x;
+          });
+        });
+      }
+      if constexpr (CH == kChainActHeavy) {
+        activation([](float* v) { sigmoid_n<16>(v); });
+        add_row(fx_slot1, fx_a1);
+      }
+    };
     // One column block: its NJ accumulator blocks A[j] through the op chain, then
     // its stores, staged-output writes and reduction partials.
     auto column_block = [&](f32x16_t(&A)[NJ], const int i) {
-      for (int o = 0; o < d.n_ops; ++o) {
+      if constexpr (CH != kChainGeneric) fixed_ops(A, i);
+      if constexpr (CH == kChainGeneric) for (int o = 0; o < d.n_ops; ++o) {
         // Lane coordinates through an opaque copy: the per-block addresses derived
         // from them are recomputed inside each op instead of being hoisted out of
         // the loop and held.
@@ -1517,13 +1612,13 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
 
 }  // namespace fuseml_gemm
 
-// Explicit instantiation of one tile variant's four kernels (bf16/f16 operands,
-// with and without reductions).
-#define FUSEML_GEMM_INSTANTIATE_ONE(C, T, R)                                                      \
+// Explicit instantiation of one tile variant's four generic kernels (bf16/f16
+// operands, with and without reductions), and of fixed-chain kernels.
+#define FUSEML_GEMM_INSTANTIATE_ONE(C, T, R, CH)                                                  \
   template __global__ void fuseml_gemm::gemm_epilogue_kernel<C.bm, C.bn, C.bk, C.stages, C.wm, C.wn, \
-                                                              C.sched, T, R>(const fuseml_gemm_desc);
-#define FUSEML_GEMM_INSTANTIATE(C)                   \
-  FUSEML_GEMM_INSTANTIATE_ONE(C, __bf16, false)      \
-  FUSEML_GEMM_INSTANTIATE_ONE(C, __bf16, true)       \
-  FUSEML_GEMM_INSTANTIATE_ONE(C, _Float16, false)    \
-  FUSEML_GEMM_INSTANTIATE_ONE(C, _Float16, true)
+                                                              C.sched, T, R, CH>(const fuseml_gemm_desc);
+#define FUSEML_GEMM_INSTANTIATE(C)                                             \
+  FUSEML_GEMM_INSTANTIATE_ONE(C, __bf16, false, fuseml_gemm::kChainGeneric)    \
+  FUSEML_GEMM_INSTANTIATE_ONE(C, __bf16, true, fuseml_gemm::kChainGeneric)     \
+  FUSEML_GEMM_INSTANTIATE_ONE(C, _Float16, false, fuseml_gemm::kChainGeneric)  \
+  FUSEML_GEMM_INSTANTIATE_ONE(C, _Float16, true, fuseml_gemm::kChainGeneric)

@@ -32,10 +32,29 @@ constexpr TileConfig kDeep = {256, 256, 64, 2, 2, 2, 3};   // 4 waves (1/SIMD), 
 constexpr TileConfig kSmall = {128, 128, 32, 4, 2, 2, 0};  // 4 waves lock-step, 66 KB LDS, 2 WG/CU
 constexpr TileConfig kDeep3 = {256, 256, 64, 2, 2, 2, 6};  // as kDeep, whole-stage fragments; K % 64 == 0
 
+// Epilogue chains compiled into kernels of their own (template parameter CH
+// of the kernel).  kChainGeneric runs the descriptor's op list through the
+// runtime op loop; every other value is one fixed op sequence, matched on the
+// host (operand kinds included) and compiled as straight-line code with no
+// per-op dispatch.  "row" is a [N] vector operand in an LDS slot, "tile" the
+// LDS-staged bf16 2-D operand; ADD keeps its alpha from the descriptor.
+enum FixedChain : int {
+  kChainGeneric = 0,
+  kChainNone = 1,          // (no ops)
+  kChainBias = 2,          // add(row)
+  kChainBiasGeluErf = 3,   // add(row), gelu(approximate='none')
+  kChainBiasGeluTanh = 4,  // add(row), gelu(approximate='tanh')
+  kChainBiasRelu = 5,      // add(row), relu
+  kChainBiasTile = 6,      // add(row), add(tile)           (bias + residual)
+  kChainActHeavy = 7,      // add(row), relu, mul(tile), sigmoid, add(row)
+  kChainRelu = 8,          // relu                          (also with reductions)
+  kNumChains = 9,
+};
+
 // The kernel (defined in gemm_epilogue_kernel.h).  SCHED selects the K-loop
 // schedule, T the GEMM operand type (__bf16 or _Float16), RED whether the
-// launch has reductions.
-template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T, bool RED>
+// launch has reductions, CH the epilogue chain (FixedChain).
+template <int BM, int BN, int BK, int S, int WM, int WN, int SCHED, typename T, bool RED, int CH>
 __global__ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg);
 
 }  // namespace fuseml_gemm

@@ -158,10 +158,22 @@ int fuseml_gemm_epilogue_supported(const fuseml_gemm_desc* desc);
  * parameter selection of kernel_launcher.py:134-306 / sram_autotuner.py. */
 int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]);
 
+/* The epilogue a launch of `desc` would compile in: 0 for the generic op loop
+ * (the descriptor's ops interpreted at run time), else the id of the fixed
+ * chain kernel (1 none, 2 bias, 3 bias+GELU(erf), 4 bias+GELU(tanh),
+ * 5 bias+ReLU, 6 bias+2-D add, 7 bias,ReLU,2-D mul,sigmoid,row add, 8 ReLU
+ * with or without reductions) — the same arithmetic as straight-line code,
+ * built for the one-wave whole-stage variant and bf16 operands.  A negative
+ * FUSEML_E* code for an invalid descriptor.  For tests and measurement; it
+ * replaces reading which Triton kernel source was generated
+ * (fuseml/codegen/kernel_generator.py:1067-1141). */
+int fuseml_gemm_epilogue_chain(const fuseml_gemm_desc* desc);
+
 /* Pin the kernel variant for every later launch in this process: "large"
  * (256x256 ping-pong), "deep" (256x256 one wave per SIMD), "deep3" (the same
- * with whole-stage fragments; K % 64 == 0, else deep), "small" (128x128), or
- * NULL / "" / "auto" for the automatic choice.  The environment variable
+ * with whole-stage fragments; K % 64 == 0, else deep), "deep3-generic"
+ * (deep3 with the generic op loop even where a fixed chain matches), "small"
+ * (128x128), or NULL / "" / "auto" for the automatic choice.  The environment variable
  * FUSEML_HIP_TILE sets the initial value; it is read once per process.  For
  * tuning sweeps and per-variant parity tests; it replaces pinning a Triton
  * autotune config (fuseml/codegen/kernel_generator.py:587-615).  Returns

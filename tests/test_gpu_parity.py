@@ -168,14 +168,16 @@ def test_reductions_parity(axis, shape):
 # schedules on every chain, on ragged edges and on K that ends mid-stage.
 # ---------------------------------------------------------------------------
 
-VARIANTS = ["large", "deep", "deep3", "small"]
+VARIANTS = ["large", "deep", "deep3", "deep3-generic", "small"]
 
 
 def _k_for(variant, K):
-    """deep3 (the one-wave schedule with whole-stage fragments) runs only for
-    K % 64 == 0 (the library falls back to deep otherwise), so its cases keep
-    the ragged M and N and round K up to a multiple of 64."""
-    return -(-K // 64) * 64 if variant == "deep3" else K
+    """deep3 (the one-wave schedule with whole-stage fragments; with the fixed
+    chain kernels where a chain matches, or the generic op loop only under
+    "deep3-generic") runs only for K % 64 == 0 (the library falls back to deep
+    otherwise), so its cases keep the ragged M and N and round K up to a
+    multiple of 64."""
+    return -(-K // 64) * 64 if variant.startswith("deep3") else K
 
 
 VARIANT_SHAPES = [
@@ -213,6 +215,99 @@ def test_variant_chain_parity(forced_variant, chain, shape):
     torch.cuda.synchronize()
     ref = ora.gemm_epilogue([_np(t) for t in inputs], left, right, steps)["tile"]
     _check_tile(out, ref, f"{forced_variant} {chain} {shape}")
+
+
+# Fixed-chain kernels (compile-time epilogues of the deep3 variant) against the
+# generic op loop of the same variant: the same arithmetic in the same order,
+# so the outputs must be bitwise equal (sums and means, accumulated by fp32
+# atomics in no fixed order across workgroups, to 1e-6 relative).
+FIXED = {
+    "none": ([], 1),
+    "bias": ([("add", 0, 0.75)], 2),
+    "bias_gelu": (CHAINS["bias_gelu"], 3),
+    "bias_gelu_tanh": (CHAINS["bias_gelu_tanh"], 4),
+    "bias_relu": (CHAINS["bias_relu"], 5),
+    "bias_residual": ([("add", 0, 1.0), ("add", 1, -1.5)], 6),
+    "act_heavy": (CHAINS["act_heavy"], 7),
+    "relu": ([("relu", -1, 1.0)], 8),
+}
+
+
+def _chain_of(L):
+    """The chain kernel id the launcher's (single) plan ran on."""
+    import ctypes
+
+    from fuseml_amd import _abi
+
+    (plan,) = L._plans.values()
+    return _abi.load_library().fuseml_gemm_epilogue_chain(ctypes.byref(plan.desc))
+
+
+@pytest.mark.parametrize("name", sorted(FIXED))
+@pytest.mark.parametrize("shape", [(600, 1024, 192), (4392, 4360, 128), (256, 512, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_fixed_chain_bitwise_equals_generic(name, shape):
+    from fuseml_amd import _abi
+
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=91)
+    ops = _operands(M, N, dtype, seed=92)
+    inputs = [t.cuda() for t in ops + [a, w.t()]]
+    left, right = len(ops), len(ops) + 1
+    steps, want = FIXED[name]
+    spec = _spec(left=left, right=right, ops=steps, out_dtype=dtype)
+    print(f"case fixed chain={name} shape={shape}", flush=True)
+    outs = {}
+    try:
+        for variant, chain in (("deep3", want), ("deep3-generic", 0)):
+            _abi.force_variant(variant)
+            L = _launcher(spec, len(inputs))
+            outs[variant] = L(*inputs)
+            torch.cuda.synchronize()
+            assert _chain_of(L) == chain, (variant, _chain_of(L))
+    finally:
+        _abi.force_variant(None)
+    assert torch.equal(outs["deep3"], outs["deep3-generic"]), f"{name}: fixed differs from generic"
+    host = [t.cpu() for t in inputs]
+    ref = ora.gemm_epilogue([_np(t) for t in host], left, right, steps)["tile"]
+    _check_tile(outs["deep3"], ref, f"fixed {name} {shape}")
+
+
+@pytest.mark.parametrize("axis", [1, 0])
+@pytest.mark.parametrize("shape", [(600, 1032, 128), (4392, 4360, 192)], ids=lambda s: "x".join(map(str, s)))
+def test_fixed_relu_reductions_equal_generic(axis, shape):
+    """The ReLU + sum/amax/mean group (C4's) on its fixed kernel against the
+    generic loop: tile and amax bitwise, sum and mean to 1e-6 relative."""
+    from fuseml_amd import _abi
+
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=93)
+    steps = [("relu", -1, 1.0)]
+    spec = _spec(left=0, right=1, ops=steps, out_dtype=dtype, store_tile=True,
+                 reductions=("sum", "amax", "mean"), reduce_axis=axis, reduce_dtypes=(torch.float32,) * 3,
+                 outputs=(("tile",), ("red", "sum"), ("red", "amax"), ("red", "mean")))
+    print(f"case fixed relu reductions axis={axis} shape={shape}", flush=True)
+    res = {}
+    try:
+        for variant, chain in (("deep3", 8), ("deep3-generic", 0)):
+            _abi.force_variant(variant)
+            L = _launcher(spec, 2)
+            res[variant] = L(a.cuda(), w.t().cuda())
+            torch.cuda.synchronize()
+            assert _chain_of(L) == chain
+    finally:
+        _abi.force_variant(None)
+    (ft, fs, fm, fmean), (gt, gs, gm, gmean) = res["deep3"], res["deep3-generic"]
+    assert torch.equal(ft, gt) and torch.equal(fm, gm)
+    assert torch.allclose(fs, gs, rtol=1e-6, atol=1e-6) and torch.allclose(fmean, gmean, rtol=1e-6, atol=1e-6)
+    ref = ora.gemm_epilogue([_np(a), _np(w.t())], 0, 1, steps, ("sum", "amax", "mean"), axis)
+    v = ref["tile"]
+    _check_tile(ft, v, "fixed relu tile")
+    _check_red(fs, ref["sum"], np.abs(v).sum(axis=axis), "sum")
+    _check_red(fm, ref["amax"], np.abs(v).max(axis=axis), "amax")
+    _check_red(fmean, ref["mean"], np.abs(v).mean(axis=axis), "mean")
 
 
 @pytest.mark.parametrize("forced_variant", VARIANTS, indirect=True)
