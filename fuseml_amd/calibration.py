@@ -1,0 +1,193 @@
+"""The measurement behind the cost model's two thresholds (fused kernel or eager).
+
+    python -m fuseml_amd.calibration [--out profiles/cost_model_calibration.json]
+
+For each group below, on one GPU, the same inputs run three ways:
+
+* ``fused``: the group through :class:`~fuseml_amd.launcher.HipKernelLauncher`
+  (one launch of the gfx950 kernel family, automatic variant);
+* ``eager``: the group's PyTorch ops (hipBLASLt's GEMM with the addmm bias in
+  its epilogue, then one elementwise kernel per remaining op);
+* ``mm``: hipBLASLt's plain GEMM alone (what eager's GEMM costs without the
+  epilogue passes).
+
+Each time is the median of HIP-event timed calls (per call: event, launch,
+event), the best of two alternating passes.  The groups are the benchmark
+configs' six GEMM groups at full size, a K sweep of one- and four-pass chains
+at 256+ tiles, and a few-tile sweep (fewer 128x128 output tiles than CUs) of a
+bias+GELU chain over K.  They replace the reference's NVIDIA tables
+(fuseml/passes/topology.py:286-571), which on ROCm fall to defaults.
+
+Each row records the chain's elementwise passes
+(:func:`fuseml_amd.compiler.epilogue_passes`), the 128x128 tile count, the
+three times, and which path won; ``tests/test_cost_model_calibration.py``
+checks that :func:`fuseml_amd.compiler.fused_beats_eager` and the few-tile
+rule of :func:`fuseml_amd.compiler.trigger_is_fusible` pick the measured
+winner on every row where the two differ by more than the tie margin.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+import sys
+import time
+from typing import Callable, Dict, List, Tuple
+
+import torch
+import torch.nn.functional as F
+
+BF = torch.bfloat16
+
+# (label, chain, M, N, K).  Chains: "bias_gelu" (addmm + GELU, 1 pass),
+# "bias_residual" (addmm + residual add, 1 pass), "bias_gelu_residual"
+# (addmm, GELU, residual add: 2 passes), "act_heavy" (addmm, ReLU, gate
+# product, sigmoid, row add: 4 passes), "relu_3red" (mm, ReLU, row sum, amax
+# and mean: 4 passes).
+CONFIG_GROUPS: List[Tuple[str, str, int, int, int]] = [
+    ("C2 G1", "bias_gelu", 16384, 4096, 1024),
+    ("C2 G2", "bias_residual", 16384, 1024, 4096),
+    ("C3", "act_heavy", 16384, 4096, 1024),
+    ("C4", "relu_3red", 8192, 8192, 2048),
+    ("C5 G1", "bias_gelu", 8192, 16384, 4096),
+    ("C5 G2", "bias_residual", 8192, 4096, 16384),
+]
+K_SWEEP: List[Tuple[str, str, int, int, int]] = (
+    [(f"bias_gelu K={k}", "bias_gelu", 16384, 4096, k) for k in (2048, 4096)]
+    + [(f"bias_residual K={k}", "bias_residual", 16384, 1024, k) for k in (1024, 2048)]
+    + [(f"bias_gelu_residual K={k}", "bias_gelu_residual", 16384, 4096, k) for k in (2048, 4096, 8192)]
+    + [(f"act_heavy K={k}", "act_heavy", 16384, 4096, k) for k in (2048, 4096, 8192)]
+    + [(f"relu_3red K={k}", "relu_3red", 8192, 8192, k) for k in (4096, 8192)]
+)
+FEW_TILES: List[Tuple[str, str, int, int, int]] = [
+    (f"few-tile {m}x{n} K={k}", "bias_gelu", m, n, k)
+    for (m, n) in ((1024, 1024), (256, 4096), (512, 4096), (2048, 2048))
+    for k in (1024, 2048, 4096, 8192)
+]
+GROUPS = CONFIG_GROUPS + K_SWEEP + FEW_TILES
+
+
+def _spec(chain: str):
+    from .epilogue import EpilogueSpec, EpiOp
+
+    if chain == "bias_gelu":
+        return EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("gelu_erf")), BF), 3
+    if chain == "bias_residual":
+        return EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("add", 3)), BF), 4
+    if chain == "bias_gelu_residual":
+        return EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("gelu_erf"), EpiOp("add", 3)), BF), 4
+    if chain == "act_heavy":
+        return EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("relu"), EpiOp("mul", 3), EpiOp("sigmoid"),
+                                   EpiOp("add", 4)), BF), 5
+    if chain == "relu_3red":
+        return EpilogueSpec(0, 1, (EpiOp("relu"),), BF, store_tile=True, reductions=("sum", "amax", "mean"),
+                            reduce_axis=1, reduce_dtypes=(torch.float32,) * 3,
+                            outputs=(("tile",), ("red", "sum"), ("red", "amax"), ("red", "mean"))), 2
+    raise ValueError(chain)
+
+
+def _inputs(chain: str, M: int, N: int, K: int, dev) -> List[torch.Tensor]:
+    g = torch.Generator().manual_seed(M * 31 + N * 7 + K)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    wt = (torch.randn(N, K, generator=g) / K ** 0.5).to(BF).to(dev).t()
+    b = (torch.rand(N, generator=g) * 0.1 - 0.05).to(BF).to(dev)
+    if chain == "bias_gelu":
+        return [b, x, wt]
+    if chain in ("bias_residual", "bias_gelu_residual"):
+        return [b, x, wt, torch.randn(M, N, generator=g).to(BF).to(dev)]
+    if chain == "act_heavy":
+        gate = torch.rand(M, N, generator=g).to(BF).to(dev)
+        return [b, x, wt, gate, (torch.rand(N, generator=g) * 0.06 - 0.03).to(BF).to(dev)]
+    return [x, wt]
+
+
+def _eager(chain: str) -> Callable:
+    if chain == "bias_gelu":
+        return lambda b, x, wt: F.gelu(torch.addmm(b, x, wt))
+    if chain == "bias_residual":
+        return lambda b, x, wt, r: torch.addmm(b, x, wt) + r
+    if chain == "bias_gelu_residual":
+        return lambda b, x, wt, r: F.gelu(torch.addmm(b, x, wt)) + r
+    if chain == "act_heavy":
+        return lambda b, x, wt, gate, row: torch.sigmoid(torch.relu(torch.addmm(b, x, wt)) * gate) + row
+
+    def relu_3red(x, wt):
+        h = torch.relu(x @ wt)
+        return h, h.sum(-1, dtype=torch.float32), h.amax(-1), h.mean(-1, dtype=torch.float32)
+
+    return relu_3red
+
+
+def _median_ms(fn: Callable[[], object], iters: int) -> float:
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def measure(groups=GROUPS, passes: int = 2, dev: str = "cuda") -> List[Dict[str, object]]:
+    from .compiler import LONG_K, MIN_TILES_LONG_K, epilogue_passes, fused_beats_eager
+    from .launcher import HipKernelLauncher
+
+    rows = []
+    for label, chain, M, N, K in groups:
+        spec, n_in = _spec(chain)
+        ins = _inputs(chain, M, N, K, dev)
+        L = HipKernelLauncher(spec, n_in)
+        eager = _eager(chain)
+        x, wt = ins[spec.left], ins[spec.right]
+        fns = {"fused": lambda: L(*ins), "eager": lambda: eager(*ins), "mm": lambda: x @ wt}
+        iters = max(20, min(400, int(2e12 / (2.0 * M * N * K) * 40)))
+        best = {k: float("inf") for k in fns}
+        with torch.no_grad():
+            for _ in range(passes):
+                for k, f in fns.items():
+                    best[k] = min(best[k], _median_ms(f, iters))
+        tiles = -(-M // 128) * -(-N // 128)
+        addmm = chain != "relu_3red"  # the other chains' GEMM is an addmm (bias in hipBLASLt's epilogue)
+        p = epilogue_passes(spec, gemm_is_addmm=addmm)
+        few = K >= LONG_K and tiles < MIN_TILES_LONG_K
+        rule = (not few) and fused_beats_eager(spec, K, dtype=BF, gemm_is_addmm=addmm)[0]
+        rows.append({"group": label, "chain": chain, "M": M, "N": N, "K": K, "passes": p, "tiles_128": tiles,
+                     "fused_ms": round(best["fused"], 4), "eager_ms": round(best["eager"], 4),
+                     "mm_ms": round(best["mm"], 4), "fused_over_eager": round(best["fused"] / best["eager"], 3),
+                     "rule_fuses": bool(rule)})
+        print(f"[calibration] {label}: fused {best['fused']:.4f} eager {best['eager']:.4f} mm {best['mm']:.4f} ms",
+              file=sys.stderr, flush=True)
+        del L, ins
+        torch.cuda.empty_cache()
+    return rows
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--out", default="", help="write the JSON here (default: stdout)")
+    ap.add_argument("--passes", type=int, default=2)
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("calibration needs a GPU", file=sys.stderr)
+        return 2
+    t0 = time.perf_counter()
+    rows = measure(passes=args.passes)
+    arch = getattr(torch.cuda.get_device_properties(0), "gcnArchName", "")
+    doc = {"device": arch, "seconds": round(time.perf_counter() - t0, 1),
+           "method": "median HIP-event time per call, best of alternating passes; same inputs for all three paths",
+           "rows": rows}
+    text = json.dumps(doc, indent=1)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+    else:
+        print(text)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -56,8 +56,11 @@ MIN_FUSION_OUTPUT_ELEMENTS = 500_000
 LONG_K = 2048
 MIN_TILES_LONG_K = 256  # 128x128 output tiles; MI355X has 256 CUs
 # Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the
-# eager path would run over the [M,N] output): measured crossover on MI355X.
-K_PER_EPILOGUE_PASS = 1024
+# eager path would run over the [M,N] output) - K_CROSSOVER_OFFSET: the
+# crossover measured on MI355X (fuseml_amd/calibration.py; the measurement is
+# profiles/cost_model_calibration.json): 1536 for one pass, 9216 for four.
+K_PER_EPILOGUE_PASS = 2560
+K_CROSSOVER_OFFSET = 1024
 # fp32 operands run as a three-term bf16 split product (K' = 3 ceil8(K)).
 SUPPORTED_GEMM_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
@@ -191,29 +194,34 @@ def epilogue_passes(spec: EpilogueSpec, gemm_is_addmm: bool = True) -> int:
 
 
 def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOGUE_PASS,
-                      dtype: Any = None, gemm_is_addmm: bool = True) -> Tuple[bool, str]:
+                      dtype: Any = None, gemm_is_addmm: bool = True,
+                      k_offset: int = K_CROSSOVER_OFFSET) -> Tuple[bool, str]:
     """The fused kernel against eager (hipBLASLt GEMM + elementwise kernels).
 
-    Measured on one MI355X, each fused group against its eager ops (same box,
-    HIP events): the fused kernel saves one HBM round trip of the [M,N] result
-    per elementwise pass, while its K loop is slower than hipBLASLt's plain
-    GEMM by about a fifth from K = 4096 on (plain GEMM 16384x1024x4096:
-    0.091 ms against the fused 0.126 ms with bias + residual; eager 0.107).
-    With one pass the fused kernel wins at K = 1024 (bias + GELU, 16384x4096:
-    0.159 against eager 0.167 ms) and loses at K = 4096 (8192x16384: 0.874
-    against 0.829 ms) and K = 16384 (bias + residual: 0.801 against 0.714 ms);
-    with four passes it wins at K = 1024 (C3: 0.201 against 0.313 ms) and
-    K = 2048 (ReLU + three row reductions: 0.269 against 0.374 ms).  Rule: fuse
-    iff K <= k_per_pass * passes; k_per_pass = 0 always fuses.
+    Measured on one MI355X by ``python -m fuseml_amd.calibration`` (each group
+    fused, eager and as a plain GEMM on the same inputs; the rows are
+    profiles/cost_model_calibration.json).  Over hipBLASLt's plain GEMM, eager
+    pays about one [M,N] HBM round trip per elementwise pass (0.06-0.07 ms per
+    pass at 16384x4096, the same at every K), while the fused kernel pays its
+    epilogue (which grows slower than the number of ops) plus a K loop that
+    falls behind hipBLASLt's as K grows.  So the crossover K grows with the
+    passes: one pass fuses at K = 1024 (bias + GELU 16384x4096: 0.157 against
+    eager 0.168 ms), ties at K = 2048 and loses from K = 4096 (8192x16384: 0.852
+    against 0.836 ms; bias + residual at K = 16384: 0.776 against 0.723 ms);
+    four passes still win at K = 8192 (0.80 against 0.90 ms).  Rule: fuse iff
+    K <= k_per_pass * passes - k_offset (2560 and 1024: K <= 1536 for one pass,
+    4096 for two, 9216 for four); k_per_pass = 0 always fuses.
 
     fp32 groups always fuse: eager runs an fp32 GEMM at the fp32 MFMA rate
     (157 TFLOP/s peak), the split product at a third of the bf16 rate."""
     if k_per_pass <= 0 or dtype == torch.float32:
         return True, "fused"
     passes = epilogue_passes(spec, gemm_is_addmm)
-    if K <= k_per_pass * passes:
+    limit = k_per_pass * passes - k_offset
+    if K <= limit:
         return True, "fused"
-    return False, f"K={K} with {passes} elementwise pass(es): eager's GEMM is faster (crossover K <= {k_per_pass} per pass)"
+    return False, (f"K={K} with {passes} elementwise pass(es): eager's GEMM is faster "
+                   f"(crossover K <= {k_per_pass} x passes - {k_offset} = {limit})")
 
 
 def build_hip_launcher(group: Any, eager_fn: Optional[Callable[..., Any]] = None, *,

@@ -86,7 +86,10 @@ int forced_variant() {
   return v;
 }
 
+int match_fixed_chain(const fuseml_gemm_desc& d);
+
 // `cus`: the device's CU count (the 256-wide variants run one workgroup per CU).
+// `d` has its flags derived (derive_flags).
 TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
   // A pinned variant (tuning sweeps and the per-variant parity tests; deep3
   // falls back to deep when K % 64 != 0).
@@ -104,12 +107,19 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
   // the faster K loop but the slower epilogue (no second wave on a SIMD to
   // overlap its latencies).  The whole-stage one wins from K = 2048 with at
   // least one full round of tiles (C4 2%, C5 4-10%, C2's second GEMM at K =
-  // 4096 and 256 tiles 3%) or from K = 8192; at K = 1024 it loses 12-16% on
-  // bias+GELU and C3's chain and ties without ops.  With K % 64 != 0 the
+  // 4096 and 256 tiles 3%) or from K = 8192.  At K = 1024 its generic op loop
+  // loses 12-16% on bias+GELU and C3's chain, but with a fixed-chain epilogue
+  // it wins on every fixed chain (3-7% on 256 to 1024 tiles; none, bias, ReLU,
+  // bias+ReLU, GELU(tanh), bias+residual, the act-heavy chain) except
+  // bias+GELU(erf), which ties or loses up to 1.5%.  With K % 64 != 0 the
   // two-stage one takes over from K = 8192.
   const int64_t large_tiles = cdiv(d.M, 256) * cdiv(d.N, 256);
   if (large_tiles < 128) return kSmall;
   if (d.K % 64 == 0 && (d.K >= 8192 || (d.K >= 2048 && large_tiles >= cus))) return kDeep3;
+  if (d.K % 64 == 0 && d.K >= 1024) {
+    const int ch = match_fixed_chain(d);
+    if (ch != kChainGeneric && ch != kChainBiasGeluErf) return kDeep3;
+  }
   return d.K >= 8192 ? kDeep : kLarge;
 }
 
@@ -448,7 +458,10 @@ int fuseml_gemm_epilogue_config(const fuseml_gemm_desc* desc, int32_t cfg[4]) {
     const int known = g_device_cus[dev].load(std::memory_order_relaxed);
     if (known > 0) cus = known;
   }
-  const TileConfig c = choose_config(*desc, cus);
+  fuseml_gemm_desc d = *desc;
+  fold_final_store(d);
+  derive_flags(d);
+  const TileConfig c = choose_config(d, cus);
   cfg[0] = c.bm;
   cfg[1] = c.bn;
   cfg[2] = c.wm * c.wn;

@@ -50,14 +50,16 @@ PROBE_KERNEL_HINT = "mfma_peak_kernel"
 
 
 def _short(name: str) -> str:
-    """gemm_epilogue_kernel<BM,BN,BK,S,WM,WN,SCHED,dtype[,red]> from the mangled
-    name (",red": the instantiation that carries the reductions)."""
-    m = re.search(r"gemm_epilogue_kernelI((?:Li\d+E)+)(DF16b|DF16_)(?:Lb([01])E)?E", name)
+    """gemm_epilogue_kernel<BM,BN,BK,S,WM,WN,SCHED,dtype[,red][,chN]> from the
+    mangled name (",red": the instantiation that carries the reductions;
+    ",chN": fixed epilogue chain N, absent for the generic op loop, chain 0)."""
+    m = re.search(r"gemm_epilogue_kernelI((?:Li\d+E)+)(DF16b|DF16_)(?:Lb([01])E)?(?:Li(\d+)E)?E", name)
     if m:
         ints = ",".join(re.findall(r"Li(\d+)E", m.group(1)))
         dtype = {"DF16b": "bf16", "DF16_": "f16"}[m.group(2)]
-        return f"gemm_epilogue_kernel<{ints},{dtype}{',red' if m.group(3) == '1' else ''}>"
-    # Demangled by the profiler: "void ns::gemm_epilogue_kernel<256, 256, ..., __bf16, true>(...)".
+        ch = f",ch{m.group(4)}" if m.group(4) not in (None, "0") else ""
+        return f"gemm_epilogue_kernel<{ints},{dtype}{',red' if m.group(3) == '1' else ''}{ch}>"
+    # Demangled by the profiler: "void ns::gemm_epilogue_kernel<256, 256, ..., __bf16, true, 3>(...)".
     # rocprofv3 demangles some instantiations with a garbled type tail (the
     # __bf16 mangling); then only the seven tile integers are kept.
     m = re.search(r"gemm_epilogue_kernel<((?:\d+, ){6}\d+), ([^()]*)>\(", name)
@@ -65,9 +67,11 @@ def _short(name: str) -> str:
         ints = m.group(1).replace(" ", "")
         tail = [t.strip() for t in m.group(2).split(",")]
         dtype = {"__bf16": "bf16", "_Float16": "f16"}.get(tail[0]) if tail else None
-        if dtype is None or len(tail) != 2 or tail[1] not in ("true", "false"):
+        if dtype is None or len(tail) not in (2, 3) or tail[1] not in ("true", "false") or \
+                (len(tail) == 3 and not tail[2].isdigit()):
             return f"gemm_epilogue_kernel<{ints},...>"
-        return f"gemm_epilogue_kernel<{ints},{dtype}{',red' if tail[1] == 'true' else ''}>"
+        ch = f",ch{tail[2]}" if len(tail) == 3 and tail[2] != "0" else ""
+        return f"gemm_epilogue_kernel<{ints},{dtype}{',red' if tail[1] == 'true' else ''}{ch}>"
     return name[:60]
 
 

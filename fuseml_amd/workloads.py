@@ -60,6 +60,22 @@ class GemmRowReductions(nn.Module):
         return h, h.sum(-1, dtype=torch.float32), h.amax(-1).float(), h.mean(-1, dtype=torch.float32)
 
 
+class ActivationHeavyMLP(nn.Module):
+    """Linear -> GELU -> * 0.5 -> + 0.125 -> Linear -> + residual: the
+    reference's activation-heavy preset block (bench_mlp_block.py:185-207),
+    two more pointwise ops absorbed into the first group."""
+
+    def __init__(self, d_model: int, d_inter: int):
+        super().__init__()
+        self.linear1 = nn.Linear(d_model, d_inter)
+        self.gelu = nn.GELU()
+        self.linear2 = nn.Linear(d_inter, d_model)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        h = self.gelu(self.linear1(x)) * 0.5 + 0.125
+        return self.linear2(h) + x
+
+
 class StackedMLP(nn.Module):
     """Blocks of TransformerMLP (bench_mlp_block.py:210-220)."""
 
@@ -154,6 +170,38 @@ def c5_stacked_mlp(scale: float = 1.0, dtype=torch.bfloat16, num_blocks: int = 4
     g = [(M, I, D), (M, D, I)] * num_blocks
     return Workload("C5_stacked_mlp_x4_bf16", model, (x,), dtype,
                     sum(2.0 * m * n * k for m, n, k in g), g)
+
+
+# The reference benchmark's presets (bench_mlp_block.py:64-153): M = batch x
+# seq rows of a [M, d_model] input, d_model -> d_intermediate; the speedups the
+# reference publishes (README.md:85-96) are quoted on these.
+REFERENCE_PRESETS: Dict[str, Tuple[str, int, int, int, int]] = {
+    # name: (workload, M, d_model, d_intermediate, blocks)
+    "small": ("mlp_block", 128, 256, 1024, 1),
+    "memory_bound": ("mlp_block", 16384, 256, 1024, 1),
+    "medium": ("mlp_block", 2048, 1024, 4096, 1),
+    "activation_heavy_memory_bound": ("activation_heavy", 16384, 256, 1024, 1),
+    "activation_heavy_medium": ("activation_heavy", 2048, 1024, 4096, 1),
+    "stacked_memory_bound": ("stacked_mlp", 8192, 512, 2048, 4),
+    "stacked_medium": ("stacked_mlp", 2048, 1024, 4096, 4),
+}
+
+
+def reference_preset(name: str, dtype=torch.bfloat16, seed: int = 0) -> Workload:
+    """One of the reference benchmark's presets in bf16: default nn.Linear
+    init after ``manual_seed(seed)``, x ~ N(0, 1) (bench_mlp_block.py:959-968)."""
+    kind, M, D, I, blocks = REFERENCE_PRESETS[name]
+    torch.manual_seed(seed)
+    if kind == "mlp_block":
+        model: nn.Module = TransformerMLP(D, I)
+    elif kind == "activation_heavy":
+        model = ActivationHeavyMLP(D, I)
+    else:
+        model = StackedMLP(D, I, blocks)
+    model = model.to(dtype).eval()
+    x = torch.randn(M, D, generator=_gen(seed)).to(dtype)
+    g = [(M, I, D), (M, D, I)] * blocks
+    return Workload(f"preset_{name}", model, (x,), dtype, sum(2.0 * m * n * k for m, n, k in g), g)
 
 
 WORKLOADS = {

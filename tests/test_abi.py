@@ -74,10 +74,27 @@ def test_supported_checks_are_host_only():
     assert "operand index" in _abi.last_error(lib)
 
 
+def _bias_gelu(d):
+    """The descriptor with a bias + GELU(erf) chain (a [N] bias operand)."""
+    d.n_operands = 1
+    o = d.operands[0]
+    o.ptr, o.stride_m, o.stride_n, o.extent, o.dtype = 0x40000, 0, 1, d.N, _abi.BF16
+    d.n_ops = 2
+    d.ops[0].kind, d.ops[0].operand, d.ops[0].scalar = _abi.OP_ADD, 0, 1.0
+    d.ops[1].kind = _abi.OP_GELU_ERF
+    return d
+
+
 def test_tile_config_choice():
+    """K = 1024, 4 tiles per CU: a chain with a fixed-chain kernel (here none)
+    runs on the one-wave whole-stage variant, bias + GELU(erf) on the ping-pong
+    one; few tiles run on 128x128 tiles."""
     lib = _abi.load_library()
     cfg = (ctypes.c_int32 * 4)()
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
+    assert tuple(cfg[:3]) == (256, 256, 4)
+    assert 128 * 1024 <= cfg[3] <= 160 * 1024
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_bias_gelu(_desc(16384, 4096, 1024))), cfg) == 0
     assert tuple(cfg[:3]) == (256, 256, 8)
     assert 128 * 1024 <= cfg[3] <= 160 * 1024
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(64, 512, 2048)), cfg) == 0
@@ -99,7 +116,7 @@ def test_force_variant_pins_and_releases():
             _abi.force_variant("huge")
     finally:
         _abi.force_variant(None)
-    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_bias_gelu(_desc(16384, 4096, 1024))), cfg) == 0
     assert tuple(cfg[:3]) == (256, 256, 8)
 
 

@@ -67,18 +67,16 @@ def _launcher(spec, n):
     return HipKernelLauncher(spec, n)
 
 
-def _config(M, N, K):
+def _launched(L):
+    """(BM, BN, waves) and the epilogue chain id of the launcher's (single) plan:
+    what its launches ran."""
     from fuseml_amd import _abi
 
     lib = _abi.load_library()
-    d = _abi.GemmDesc()
-    d.M, d.N, d.K = M, N, K
-    d.a, d.lda, d.b, d.ldb = 0x10000, K, 0x20000, K
-    d.ab_dtype = _abi.BF16
-    d.out.ptr, d.out.ld, d.out.dtype = 0x30000, N, _abi.BF16
+    (plan,) = L._plans.values()
     cfg = (ctypes.c_int32 * 4)()
-    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(d), cfg) == 0
-    return tuple(cfg[:3])
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(plan.desc), cfg) == 0
+    return tuple(cfg[:3]), lib.fuseml_gemm_epilogue_chain(ctypes.byref(plan.desc))
 
 
 def _compile(model, **kw):
@@ -108,12 +106,14 @@ def test_c3_full_size_launcher():
     wl = c3_activation_heavy()
     m = wl.model
     x, g = wl.inputs
-    assert _config(16384, 4096, 1024) == (256, 256, 8)  # ping-pong, 4 rounds of 256 tiles
     spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("relu"), EpiOp("mul", 3), EpiOp("sigmoid"),
                                EpiOp("add", 4)), torch.bfloat16)
+    L = _launcher(spec, 5)
     with torch.no_grad():
-        y = _launcher(spec, 5)(m.linear.bias.cuda(), x.cuda(), m.linear.weight.t().cuda(), g.cuda(), m.row.cuda())
+        y = L(m.linear.bias.cuda(), x.cuda(), m.linear.weight.t().cuda(), g.cuda(), m.row.cuda())
     torch.cuda.synchronize()
+    # one-wave whole-stage variant, 4 rounds of 256 tiles, the act-heavy fixed chain
+    assert _launched(L) == ((256, 256, 4), 7)
     rows = _rows(16384)
     _close(y[torch.as_tensor(rows).cuda()], _c3_ref(wl, rows), "C3")
 
@@ -165,14 +165,15 @@ def test_c4_full_size_launcher(c4_oracle):
 
     _case("C4 full size, launcher (deep3, 4 rounds)")
     wl, ref, scales = c4_oracle
-    assert _config(8192, 8192, 2048) == (256, 256, 4)
     spec = EpilogueSpec(0, 1, (EpiOp("relu"),), torch.bfloat16, store_tile=True,
                         reductions=("sum", "amax", "mean"), reduce_axis=1,
                         reduce_dtypes=(torch.float32,) * 3,
                         outputs=(("red", "sum"), ("red", "amax"), ("red", "mean"), ("tile",)))
+    L = _launcher(spec, 2)
     with torch.no_grad():
-        s, mx, mean, h = _launcher(spec, 2)(wl.inputs[0].cuda(), wl.model.linear.weight.t().cuda())
+        s, mx, mean, h = L(wl.inputs[0].cuda(), wl.model.linear.weight.t().cuda())
     torch.cuda.synchronize()
+    assert _launched(L) == ((256, 256, 4), 8)  # deep3, the ReLU (+ reductions) fixed chain
     _check_c4(h, s, mx, mean, ref, scales, "C4")
 
 

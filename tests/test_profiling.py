@@ -107,6 +107,11 @@ def test_kernel_names_with_the_reduction_flag():
     assert _short(base + "DF16_Lb1EEEv16fuseml_gemm_desc") == "gemm_epilogue_kernel<256,256,64,2,2,2,6,f16,red>"
     assert _short(GEMM) == "gemm_epilogue_kernel<256,256,32,4,2,4,1,bf16>"
     assert _short("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
+    # the epilogue-chain template argument: chain 0 (generic loop) is not shown
+    assert _short(base + "DF16bLb0ELi0EEEv16fuseml_gemm_desc") == "gemm_epilogue_kernel<256,256,64,2,2,2,6,bf16>"
+    assert _short(base + "DF16bLb0ELi3EEEv16fuseml_gemm_desc") == "gemm_epilogue_kernel<256,256,64,2,2,2,6,bf16,ch3>"
+    assert _short(base + "DF16bLb1ELi8EEEv16fuseml_gemm_desc") == \
+        "gemm_epilogue_kernel<256,256,64,2,2,2,6,bf16,red,ch8>"
 
 
 def test_kernel_names_demangled_by_the_profiler():
@@ -119,6 +124,8 @@ def test_kernel_names_demangled_by_the_profiler():
     assert _short(named) == "gemm_epilogue_kernel<256,256,32,4,2,4,1,bf16>"
     dem = "void fuseml_gemm::gemm_epilogue_kernel<256, 256, 64, 2, 2, 2, 6, __bf16, true>(fuseml_gemm_desc)"
     assert _short(dem) == "gemm_epilogue_kernel<256,256,64,2,2,2,6,bf16,red>"
+    dem_ch = "void fuseml_gemm::gemm_epilogue_kernel<256, 256, 64, 2, 2, 2, 6, __bf16, false, 7>(fuseml_gemm_desc)"
+    assert _short(dem_ch) == "gemm_epilogue_kernel<256,256,64,2,2,2,6,bf16,ch7>"
     garbled = "void fuseml_gemm::gemm_epilogue_kernel<256, 256, 64, 2, 2, 2, 6, bool _Accum, bool, E>(fuseml_gemm_desc)"
     assert _short(garbled) == "gemm_epilogue_kernel<256,256,64,2,2,2,6,...>"
 
