@@ -75,6 +75,47 @@ class _NoFusionPossible(Exception):
     """No profitable fusion: return the original forward (no AOT overhead)."""
 
 
+def aot_wrapper_is_identity(meta: Any, n_graph_inputs: int, n_call_inputs: int) -> Tuple[bool, str]:
+    """Whether AOTAutograd's runtime wrapper around an inference graph would
+    only call it: no input is mutated, no output aliases an input or an
+    intermediate, no effect tokens, RNG functionalization, tensor subclasses,
+    dynamic output dims or grad-mode changes, and the graph takes exactly the
+    call's inputs (no deduplicated or synthetic-base inputs).  ``meta`` is the
+    ``ViewAndMutationMeta`` AOTAutograd hands the forward compiler through the
+    tracing context.  Then the graph's forward can be returned to Dynamo
+    directly: per call that saves the wrapper's Python (about 20 us on the
+    MI355X box's host, more than a kernel of the reference's smaller presets
+    takes), with the same results."""
+    if meta is None:
+        return False, "no AOT metadata"
+    try:
+        from torch._functorch._aot_autograd.schemas import OutputType, PlainTensorMeta
+    except ImportError:  # pragma: no cover - other torch layouts
+        return False, "AOT schemas not importable"
+    checks = [
+        (not getattr(meta, "is_train", True), "training graph"),
+        (n_graph_inputs == n_call_inputs, f"graph takes {n_graph_inputs} inputs for {n_call_inputs}"),
+        (getattr(meta, "num_mutated_inp_runtime_indices", 1) == 0, "mutated inputs"),
+        (not any(i.mutates_data or i.mutates_metadata or i.mutates_storage_metadata
+                 for i in getattr(meta, "input_info", [None]) if i is not None), "mutated inputs"),
+        (getattr(meta, "num_intermediate_bases", 1) == 0, "intermediate bases"),
+        (getattr(meta, "num_outputs_aliased", 1) == 0, "aliased outputs"),
+        (all(o.output_type == OutputType.non_alias for o in getattr(meta, "output_info", [])), "aliased outputs"),
+        (not getattr(meta, "tokens", {1: 1}), "effect tokens"),
+        (not getattr(meta, "is_rng_op_functionalized", True), "functionalized RNG"),
+        (not getattr(meta, "dynamic_outputs", True), "dynamic outputs"),
+        (getattr(meta, "grad_enabled_mutation", 0) is None, "grad-mode mutation"),
+        (all(isinstance(s, (PlainTensorMeta, int)) for s in getattr(meta, "subclass_inp_meta", [None])),
+         "tensor subclass inputs"),
+        (all(isinstance(s, (PlainTensorMeta, int)) for s in getattr(meta, "subclass_fw_graph_out_meta", [None])),
+         "tensor subclass outputs"),
+    ]
+    for ok, why in checks:
+        if not ok:
+            return False, why
+    return True, "identity"
+
+
 def _meta(node: Any):
     if not isinstance(node, torch.fx.Node):
         return None
@@ -139,6 +180,24 @@ def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSIO
     return True, "fused"
 
 
+def _direct_forward(fwd: Callable, params_flat: List[torch.Tensor]) -> Callable:
+    """The fused ATen graph's forward, called as AOTAutograd's inference wrapper
+    calls it (lifted parameters first, autograd off during the call)."""
+    if params_flat:
+        def forward(*args):
+            if torch.is_grad_enabled():
+                with torch.no_grad():
+                    return fwd(*params_flat, *args)
+            return fwd(*params_flat, *args)
+    else:
+        def forward(*args):
+            if torch.is_grad_enabled():
+                with torch.no_grad():
+                    return fwd(*args)
+            return fwd(*args)
+    return forward
+
+
 class EagerGroupLauncher:
     """Callable that runs a group's original nodes (no fused kernel).
 
@@ -150,9 +209,12 @@ class EagerGroupLauncher:
     def __init__(self, module: torch.fx.GraphModule) -> None:
         self.__name__ = "fuseml_eager_group"
         self._module = module
+        # The generated forward itself: nn.Module.__call__'s hook machinery
+        # adds host time per call and a group module has no hooks.
+        self._forward = getattr(module, "forward", module)
 
     def __call__(self, *args):
-        return self._module(*args)
+        return self._forward(*args)
 
 
 _EagerGroup = EagerGroupLauncher
@@ -272,8 +334,14 @@ class FuseMLCompiler:
                  min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
                  min_tiles_long_k: int = MIN_TILES_LONG_K,
                  k_per_epilogue_pass: int = K_PER_EPILOGUE_PASS,
-                 require_gfx950: bool = True) -> None:
+                 require_gfx950: bool = True, direct_dispatch: bool = True) -> None:
         self.registry = registry
+        # Return the fused graph's forward to Dynamo without AOTAutograd's
+        # runtime wrapper when that wrapper would only call it
+        # (aot_wrapper_is_identity); `dispatch` records which path each
+        # compiled graph got ("direct" or "aot: <reason>").
+        self.direct_dispatch = direct_dispatch
+        self.dispatch: List[str] = []
         self.fuse_sibling_reductions = fuse_sibling_reductions
         self.fuse_leading_views = fuse_leading_views
         self.fuse_mlp_block = fuse_mlp_block
@@ -289,16 +357,41 @@ class FuseMLCompiler:
 
     # ------------------------------------------------------------------
     def __call__(self, gm: torch.fx.GraphModule, example_inputs: List[torch.Tensor]) -> Callable:
-        def _aten_compiler(aten_gm: torch.fx.GraphModule, aten_inputs: List[torch.Tensor]):
-            return make_boxed_func(self._compile_aten_graph(aten_gm, aten_inputs))
+        captured: Dict[str, Any] = {}
 
+        def _aten_compiler(aten_gm: torch.fx.GraphModule, aten_inputs: List[torch.Tensor]):
+            from torch._guards import TracingContext
+
+            fwd = self._compile_aten_graph(aten_gm, aten_inputs)
+            ctx = TracingContext.try_get()
+            captured.update(fwd=fwd, n_graph_inputs=len(aten_inputs),
+                            meta=getattr(ctx, "fw_metadata", None) if ctx is not None else None)
+            return make_boxed_func(fwd)
+
+        # What AOTAutograd prepends to every call: the Dynamo graph's own
+        # parameters and buffers (aot_module_simplified lifts them).
+        params_flat = [t for _, t in gm.named_parameters(remove_duplicate=False)] + \
+                      [t for _, t in gm.named_buffers(remove_duplicate=False)]
+        amp = torch._C._is_any_autocast_enabled()
         try:
-            return aot_module_simplified(gm, example_inputs, fw_compiler=_aten_compiler)
+            compiled = aot_module_simplified(gm, example_inputs, fw_compiler=_aten_compiler)
         except _NoFusionPossible as exc:
             self.fusion_applied = False
             self.fusion_strategy = "none"
             logger.info("bypassing AOT lowering — %s", exc)
             return gm.forward
+        if not self.direct_dispatch or "fwd" not in captured:
+            self.dispatch.append("aot: direct dispatch off")
+            return compiled
+        ok, why = aot_wrapper_is_identity(captured["meta"], captured["n_graph_inputs"],
+                                          len(params_flat) + len(example_inputs))
+        if ok and amp:
+            ok, why = False, "traced under autocast"
+        if not ok:
+            self.dispatch.append(f"aot: {why}")
+            return compiled
+        self.dispatch.append("direct")
+        return _direct_forward(captured["fwd"], params_flat)
 
     # ------------------------------------------------------------------
     def _device_ok(self, inputs: List[Any]) -> bool:

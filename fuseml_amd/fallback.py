@@ -55,11 +55,12 @@ class EagerFallbackGuard:
     def is_oom(exc: BaseException) -> bool:
         return "out of memory" in str(exc).lower()
 
-    def execute(self, launch_fn: Callable[[], Any], inputs: Sequence[Any]) -> Any:
+    def execute(self, launch_fn: Callable[..., Any], inputs: Sequence[Any]) -> Any:
+        """``launch_fn(*inputs)``, or the eager path after a recoverable error."""
         try:
             if os.environ.get(FORCE_FAIL_ENV, "") not in ("", "0"):
                 raise ForcedFailure(f"{FORCE_FAIL_ENV} set")
-            return launch_fn()
+            return launch_fn(*inputs)
         except Exception as exc:  # noqa: BLE001 - filtered below
             if not self.is_recoverable(exc):
                 raise

@@ -76,13 +76,49 @@ def _distinct_bytes(tensors: Sequence[torch.Tensor]) -> int:
     return total
 
 
+# 8-byte word index of each pointer / leading-dimension field of the
+# descriptor: a call writes them through a flat uint64 view of the structure
+# (one C-level store each) instead of through ctypes field accessors.
+_WORD = 8
+_W_A = _abi.GemmDesc.a.offset // _WORD
+_W_LDA = _abi.GemmDesc.lda.offset // _WORD
+_W_B = _abi.GemmDesc.b.offset // _WORD
+_W_LDB = _abi.GemmDesc.ldb.offset // _WORD
+_W_OUT = (_abi.GemmDesc.out.offset + _abi.Output.ptr.offset) // _WORD
+
+
+def _w_operand(i: int) -> int:
+    return (_abi.GemmDesc.operands.offset + i * ctypes.sizeof(_abi.Operand) + _abi.Operand.ptr.offset) // _WORD
+
+
+def _w_extra(i: int) -> int:
+    return (_abi.GemmDesc.extra.offset + i * ctypes.sizeof(_abi.Output) + _abi.Output.ptr.offset) // _WORD
+
+
+def _w_reduce(slot: int) -> int:
+    return _abi.GemmDesc.reduce_out.offset // _WORD + slot
+
+
+assert all(o % _WORD == 0 for o in (_abi.GemmDesc.a.offset, _abi.GemmDesc.operands.offset,
+                                     ctypes.sizeof(_abi.Operand), _abi.GemmDesc.out.offset,
+                                     _abi.GemmDesc.extra.offset, ctypes.sizeof(_abi.Output),
+                                     _abi.GemmDesc.reduce_out.offset, ctypes.sizeof(_abi.GemmDesc)))
+
+
 class _Plan:
     """What a launch needs that depends only on the input signature (shapes,
     strides, dtypes): the descriptor with every non-pointer field filled, M/N/K,
     and for each operand slot the input it comes from and whether it must be
-    rebuilt per call (a dtype conversion or a broadcast that merging copies)."""
+    rebuilt per call (a dtype conversion or a broadcast that merging copies).
 
-    __slots__ = ("desc", "M", "N", "K", "neg", "operands", "nbytes", "k_split")
+    ``fast``: a call needs only the pointers (no negative strides, no operand
+    rebuilt per call, no fp32 split, a non-empty output), written through
+    ``words``, the descriptor as uint64 words; ``a_ok`` / ``b_ok``: the GEMM
+    operands' strides are K-major as the kernel reads them (their base
+    alignment is still checked per call)."""
+
+    __slots__ = ("desc", "M", "N", "K", "neg", "operands", "nbytes", "k_split", "fast", "words", "desc_ref",
+                 "a_ok", "b_ok", "lda", "ldb", "op_words", "red_words", "extra_words", "single_tile")
 
     def __init__(self) -> None:
         self.desc = _abi.GemmDesc()
@@ -93,6 +129,15 @@ class _Plan:
         self.k_split = 0
         self.operands: List[Tuple[int, bool]] = []  # (input index, rebuilt per call)
         self.nbytes: Optional[int] = None  # algorithmic bytes, for the timing hook
+        self.fast = False
+        self.words = (ctypes.c_uint64 * (ctypes.sizeof(_abi.GemmDesc) // _WORD)).from_buffer(self.desc)
+        self.desc_ref = ctypes.byref(self.desc)
+        self.a_ok = self.b_ok = False
+        self.lda = self.ldb = 0
+        self.op_words: List[Tuple[int, int]] = []     # (descriptor word, input index)
+        self.red_words: List[Tuple[int, str]] = []    # (descriptor word, reduction name)
+        self.extra_words: List[int] = []
+        self.single_tile = False
 
 
 class HipKernelLauncher:
@@ -217,6 +262,17 @@ class HipKernelLauncher:
             mask |= _abi.RED_BITS[name]
         d.reduce_mask = mask
         d.reduce_axis = spec.reduce_axis
+        # The per-call fast path (see _Plan).
+        if not plan.k_split:
+            plan.a_ok = a.stride(1) == 1 and a.stride(0) % 8 == 0 and (a.stride(0) >= K or M == 1)
+            plan.b_ok = b.stride(0) == 1 and b.stride(1) % 8 == 0 and (b.stride(1) >= K or N == 1)
+            plan.lda, plan.ldb = a.stride(0), b.stride(1)
+        plan.op_words = [(_w_operand(i), idx) for i, (idx, _) in enumerate(plan.operands)]
+        plan.red_words = [(_w_reduce(_abi.RED_SLOT[name]), name) for name in spec.reductions]
+        plan.extra_words = [_w_extra(i) for i in range(len(spec.extra_dtypes))]
+        plan.single_tile = spec.outputs == (("tile",),) and not spec.output_shapes and spec.store_tile
+        plan.fast = (not plan.neg and not plan.k_split and M > 0 and N > 0
+                     and not any(rebuild for _, rebuild in plan.operands))
         return plan
 
     def launch(self, *inputs: torch.Tensor) -> Any:
@@ -228,6 +284,71 @@ class HipKernelLauncher:
         if plan is None:
             plan = self._make_plan(inputs)
             self._plans[key] = plan
+        # (tests may bind a recorder as the library: the general path, which
+        # assumes no device, serves those)
+        if plan.fast and self.timing_events is None and isinstance(self._lib, ctypes.CDLL):
+            return self._launch_fast(plan, inputs)
+        return self._launch_general(plan, inputs)
+
+    def _launch_fast(self, plan: _Plan, inputs: Sequence[torch.Tensor]) -> Any:
+        """A call whose plan needs only pointers: the same checks, allocations
+        and C call as the general path, with the descriptor written word by
+        word."""
+        spec = self.spec
+        a, b = inputs[spec.left], inputs[spec.right]
+        dev = a.get_device()
+        if dev < 0 or any(inputs[i].get_device() != dev for i in self._used):
+            raise _abi.FuseMLHipError(
+                _abi.EINVAL, f"inputs on {sorted({str(inputs[i].device) for i in self._used})}: "
+                "every tensor must be on the launch's GPU")
+        w = plan.words
+        pa, pb = a.data_ptr(), b.data_ptr()
+        if plan.a_ok and pa % 16 == 0:
+            w[_W_LDA] = plan.lda
+        else:
+            a = _k_major_left(a)
+            pa = a.data_ptr()
+            w[_W_LDA] = a.stride(0)
+        if plan.b_ok and pb % 16 == 0:
+            w[_W_LDB] = plan.ldb
+        else:
+            b = _k_major_right(b)
+            pb = b.data_ptr()
+            w[_W_LDB] = b.stride(1)
+        w[_W_A] = pa
+        w[_W_B] = pb
+        for wi, idx in plan.op_words:
+            w[wi] = inputs[idx].data_ptr()
+        device = a.device
+        M, N = plan.M, plan.N
+        tile = None
+        if spec.store_tile:
+            tile = torch.empty((M, N), dtype=spec.out_dtype, device=device)
+            w[_W_OUT] = tile.data_ptr()
+        else:
+            w[_W_OUT] = 0
+        extras = []
+        for wi, dt in zip(plan.extra_words, spec.extra_dtypes):
+            t = torch.empty((M, N), dtype=dt, device=device)
+            w[wi] = t.data_ptr()
+            extras.append(t)
+        reds = {}
+        if plan.red_words:
+            red_len = M if spec.reduce_axis == 1 else N
+            for wi, name in plan.red_words:
+                t = torch.empty((red_len,), dtype=torch.float32, device=device)
+                w[wi] = t.data_ptr()
+                reds[name] = t
+        rc = self._lib.fuseml_gemm_epilogue(plan.desc_ref, torch._C._cuda_getCurrentRawStream(dev))
+        if rc != _abi.OK:
+            raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
+        self.launch_count += 1
+        if plan.single_tile:
+            return tile
+        return self._assemble(tile, extras, reds)
+
+    def _launch_general(self, plan: _Plan, inputs: Sequence[torch.Tensor]) -> Any:
+        spec = self.spec
         if plan.neg:
             inputs = tuple(t.contiguous() if isinstance(t, torch.Tensor) else t for t in inputs)
         M, N = plan.M, plan.N
@@ -345,5 +466,5 @@ class HipKernelLauncher:
         if len(inputs) != self._n_inputs:
             raise ValueError(f"Expected {self._n_inputs} input tensor(s), got {len(inputs)}.")
         if self._fallback_guard is not None:
-            return self._fallback_guard.execute(lambda: self.launch(*inputs), inputs)
+            return self._fallback_guard.execute(self.launch, inputs)
         return self.launch(*inputs)

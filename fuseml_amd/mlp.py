@@ -127,7 +127,7 @@ class HipMlpLauncher:
         if len(inputs) != self.N_INPUTS:
             raise ValueError(f"Expected {self.N_INPUTS} inputs (x, t(W1), b1, t(W2), b2, r), got {len(inputs)}.")
         if self._guard is not None:
-            return self._guard.execute(lambda: self.launch(*inputs), inputs)
+            return self._guard.execute(self.launch, inputs)
         return self.launch(*inputs)
 
 

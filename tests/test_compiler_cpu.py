@@ -295,3 +295,69 @@ def test_long_k_groups_route_to_eager(recorded):
         out = _compile(m, be)(x)
     assert torch.allclose(out.float(), m(x).float(), atol=1e-2)
     assert recorded.built == [] and be.fusion_strategy == "eager"
+
+
+class _MutatesInput(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.lin = nn.Linear(64, 256)
+
+    def forward(self, x):
+        x.mul_(2.0)
+        return F.gelu(self.lin(x))
+
+
+class _ReturnsInputView(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.lin = nn.Linear(64, 256)
+
+    def forward(self, x):
+        return F.gelu(self.lin(x)), x.view(-1)
+
+
+def test_direct_dispatch_when_aot_wrapper_is_identity(recorded):
+    """An inference graph with no mutated inputs and no aliased outputs: the
+    backend returns the fused graph's forward itself (no AOTAutograd runtime
+    wrapper), and the compiled module still equals eager, also when called
+    with autograd on."""
+    torch.manual_seed(0)
+    m = TransformerMLP(64, 256).to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        c = _compile(m, be)
+        out = c(x)
+        assert torch.allclose(out.float(), m(x).float(), atol=1e-2)
+    assert be.dispatch == ["direct"] and be.fusion_applied
+    off = FuseMLCompiler(require_gfx950=False, min_output_elements=0, direct_dispatch=False)
+    with torch.no_grad():
+        assert torch.equal(_compile(m, off)(x), out)
+    assert off.dispatch == ["aot: direct dispatch off"]
+
+
+def test_mutated_input_keeps_the_aot_wrapper(recorded):
+    torch.manual_seed(0)
+    m = _MutatesInput().to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    x_ref = x.clone()
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+        ref = m(x_ref)
+    assert torch.equal(x, x_ref)  # the input mutation was applied by the wrapper
+    assert torch.allclose(out.float(), ref.float(), atol=1e-2)
+    assert be.dispatch and be.dispatch[0].startswith("aot: mutated inputs")
+
+
+def test_output_aliasing_an_input_keeps_the_aot_wrapper(recorded):
+    torch.manual_seed(0)
+    m = _ReturnsInputView().to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=0)
+    with torch.no_grad():
+        y, v = _compile(m, be)(x)
+        ry, _ = m(x)
+    assert torch.allclose(y.float(), ry.float(), atol=1e-2)
+    assert v.data_ptr() == x.data_ptr() and v.shape == (32 * 64,)  # still a view of the input
+    assert be.dispatch and be.dispatch[0].startswith("aot: aliased outputs")

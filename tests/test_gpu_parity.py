@@ -882,3 +882,29 @@ def test_c5_block_full_size_sampled_rows():
     _check_tile(y[torch.as_tensor(rows).cuda()], ref, "C5 block")
     ref_h = ora.gelu_erf(ora_w.linear(_np(x)[rows], _np(W1), _np(b1)))
     _check_tile(h[torch.as_tensor(rows).cuda()], ref_h, "C5 G1")
+
+
+def test_same_signature_aligned_then_misaligned_operand():
+    """One launch plan serves every call with the same shapes, strides and
+    dtypes; the operands' base alignment is checked per call.  The second call
+    passes A as a view 2 bytes off a 16-byte boundary (same strides, same
+    plan): the launcher copies it to an aligned buffer and the result still
+    matches the oracle, as does a W whose view starts 2 bytes in."""
+    M, N, K = 300, 520, 136
+    dtype = torch.bfloat16
+    steps = CHAINS["bias_gelu"]
+    spec = _spec(left=1, right=2, ops=steps, out_dtype=dtype)
+    L = _launcher(spec, 3)
+    bias = (torch.rand(N, generator=_gen(95)) - 0.5).to(dtype)
+    print("case aligned then misaligned operands", flush=True)
+    for shift in (0, 1):
+        big_a = torch.randn(M, K + 8, generator=_gen(96 + shift)).to(dtype)
+        big_w = (torch.randn(N, K + 8, generator=_gen(98 + shift)) / K ** 0.5).to(dtype)
+        a_dev, w_dev = big_a.cuda()[:, shift:shift + K], big_w.cuda()[:, shift:shift + K]
+        assert (a_dev.data_ptr() % 16 == 0) == (shift == 0)
+        out = L(bias.cuda(), a_dev, w_dev.t())
+        torch.cuda.synchronize()
+        host = [bias, big_a[:, shift:shift + K], big_w[:, shift:shift + K].t()]
+        ref = ora.gemm_epilogue([_np(t) for t in host], 1, 2, steps)["tile"]
+        _check_tile(out, ref, f"shift {shift}")
+    assert len(L._plans) == 1 and L.launch_count == 2
