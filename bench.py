@@ -26,6 +26,14 @@ Rank 0 prints one JSON line carrying:
   output at sampled rows against a float32 PyTorch reference (tiles rtol/atol
   2e-2, reductions 1e-2 relative; bench_mlp_block.py:453-485), with eager
   bf16's own error beside it as calibration;
+* ``reference_presets`` — the presets the reference publishes its speedups on
+  (bench_mlp_block.py:64-153, README.md:85-96): each timed as the reference's
+  harness times it (events around one forward, a synchronisation after each,
+  median), eager against ``torch.compile(backend=FuseMLCompiler())`` with the
+  default cost model, against every group fused (cost model off) and against
+  the single-kernel MLP block where it applies, with a correctness gate
+  (atol 5e-2, rtol 2e-2 against a float32 forward, the reference's gate) and
+  the whole-forward HBM bytes of each path counted from the shapes;
 * ``fp32_block`` — the C2 block in fp32 (not a benchmark config): compiled,
   both groups as bf16 split products, against eager fp32, with errors
   against float64 at sampled rows;
@@ -83,6 +91,9 @@ def _parse():
     p.add_argument("--eager-only", action="store_true",
                    help="run only the eager leg of --workload (rocprof counter runs of the eager module)")
     p.add_argument("--cpu-iters", type=int, default=5)
+    p.add_argument("--presets", default="memory_bound,medium,activation_heavy_memory_bound,"
+                   "activation_heavy_medium,stacked_memory_bound,stacked_medium",
+                   help="reference presets to time ('' to skip; --configs '' skips them too)")
     p.add_argument("--settle-s", type=float, default=0.5,
                    help="untimed seconds of the step before its warm-up steps (the clock ramps up "
                         "over the first ~100 ms of load)")
@@ -378,6 +389,112 @@ def _config_detail(name, args, dev, peak_tflops, flush):
             out["compiled"] = comp
     del wl, stages, st0, last
     torch.cuda.empty_cache()
+    return out
+
+
+def preset_traffic(kind: str, M: int, D: int, I: int, blocks: int) -> dict:
+    """HBM bytes of one forward of a reference preset (bf16, every tensor read
+    or written once per kernel that touches it), per path:
+
+    * eager: addmm (x, W1, b1 -> t), GELU (t -> t), for the activation-heavy
+      block * 0.5 and + 0.125 (t -> t each), addmm (t, W2, b2 -> u), + x (u, x -> y);
+    * fused (two launches per block): (x, W1, b1 -> h), (h, W2, b2, x -> y);
+    * single-kernel MLP: (x, W1, b1, W2, b2 -> y), x read once as input and residual;
+    * compulsory: the forward's input, every weight and bias, its output.
+
+    "eliminated" is 1 - (path - compulsory) / (eager - compulsory): the share
+    of the intermediate traffic the path removes."""
+    e = 2  # bf16
+    wts = D * I + I + I * D + D
+    mi, md = M * I, M * D
+    extra_eager_passes = 2 if kind == "activation_heavy" else 0
+    eager = (md + D * I + I + mi) + 2 * mi + extra_eager_passes * 2 * mi + (mi + I * D + D + md) + 3 * md
+    fused = (md + D * I + I + mi) + (mi + I * D + D + md + md)
+    single = md + wts + md
+    eager, fused, single = blocks * eager * e, blocks * fused * e, blocks * single * e
+    comp = (md + blocks * wts + md) * e
+    out = {"eager_bytes": eager, "fused_bytes": fused, "compulsory_bytes": comp,
+           "fused_eliminated": round(1 - (fused - comp) / (eager - comp), 4),
+           "fused_total_saved": round(1 - fused / eager, 4)}
+    if kind != "activation_heavy":
+        out.update(single_kernel_bytes=single, single_kernel_eliminated=round(1 - (single - comp) / (eager - comp), 4))
+    return out
+
+
+def _time_sync(fn, args, warmup=25):
+    """The reference harness's timing (bench_mlp_block.py:544-590): an event
+    pair around one call and a synchronisation after each; median over at
+    least args.min_iters calls and args.min_seconds."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    t0 = time.perf_counter()
+    while True:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+        el = time.perf_counter() - t0
+        if len(times) >= args.min_iters and (el >= args.min_seconds or el >= args.max_seconds):
+            break
+    return _quartiles(times)
+
+
+def _presets(args, dev):
+    """The reference's presets: eager, compiled (default cost model), every group
+    fused, and the single-kernel MLP block, timed and checked the reference's way."""
+    from fuseml_amd.compiler import FuseMLCompiler
+    from fuseml_amd.mlp import HipMlpLauncher
+    from fuseml_amd.workloads import REFERENCE_PRESETS, reference_preset
+
+    out = {}
+    for name in [p for p in args.presets.split(",") if p]:
+        print(f"[bench] preset {name}", file=sys.stderr, flush=True)
+        kind, M, D, I, blocks = REFERENCE_PRESETS[name]
+        wl = reference_preset(name).to(dev)
+        x = wl.inputs[0]
+        m = wl.model
+        res = {"workload": kind, "M": M, "d_model": D, "d_intermediate": I, "blocks": blocks,
+               "gflop": round(wl.flops / 1e9, 1), "traffic": preset_traffic(kind, M, D, I, blocks)}
+        with torch.no_grad():
+            ref = m.float()(x.float())
+            m.to(torch.bfloat16)
+
+            def gate(y):
+                err = (y.float() - ref).abs()
+                ok = bool((err <= 5e-2 + 2e-2 * ref.abs()).all())
+                return {"max_abs_err": round(float(err.max()), 4), "pass": ok}
+
+            res["eager"] = _time_sync(lambda: m(x), args)
+            res["eager"]["check"] = gate(m(x))
+            paths = {"compiled": {}, "all_fused": dict(k_per_epilogue_pass=0, min_tiles_long_k=0,
+                                                       min_output_elements=0)}
+            if kind != "activation_heavy":
+                paths["single_kernel_mlp"] = dict(fuse_mlp_block=True, k_per_epilogue_pass=0, min_tiles_long_k=0,
+                                                  min_output_elements=0)
+            for label, kw in paths.items():
+                torch._dynamo.reset()
+                be = FuseMLCompiler(**kw)
+                c = torch.compile(m, backend=be)
+                y = c(x)
+                torch.cuda.synchronize()
+                n_mlp = sum(1 for L in be.launchers if isinstance(L, HipMlpLauncher))
+                if label == "single_kernel_mlp" and n_mlp == 0:
+                    continue
+                r = _time_sync(lambda: c(x), args)
+                r.update(check=gate(y), fusion_strategy=be.fusion_strategy,
+                         fused_launchers=len({id(L) for L in be.launchers}), dispatch=be.dispatch[:1],
+                         speedup_vs_eager=round(res["eager"]["median_ms"] / r["median_ms"], 3))
+                if label == "single_kernel_mlp":
+                    r["single_kernel_launchers"] = n_mlp
+                res[label] = r
+        out[name] = res
+        del wl, m, x, ref
+        torch._dynamo.reset()
+        torch.cuda.empty_cache()
     return out
 
 
@@ -773,6 +890,7 @@ def main():
         configs[c] = _config_detail(c, args, dev, peak["tflops"], flush)
     del flush
     torch.cuda.empty_cache()
+    presets = _presets(args, dev) if args.presets and args.configs else None
     fp32 = None
     if args.configs and not args.no_fp32:
         print("[bench] fp32 block", file=sys.stderr, flush=True)
@@ -827,6 +945,7 @@ def main():
         # the all-HIP pipeline's HBM bytes against the eager module's (committed counter summaries)
         "hbm_traffic": _hbm_traffic(name, [tuple(g) for g in _gemms_of(name)]),
         "configs": configs,
+        "reference_presets": presets,
         "fp32_block": fp32,
         "cpu_baseline": cpu,
     }

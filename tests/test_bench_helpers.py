@@ -52,3 +52,35 @@ def test_mfma_busy_from_committed_summaries():
             f = b._mfma_busy(w, i)
             assert f is not None and 0.1 < f < 1.0, (w, i, f)
     assert b._mfma_busy("nope", 0) is None
+
+
+def test_preset_traffic_matches_the_c2_table():
+    """The MLP block at C2's shape (16384; 1024 -> 4096) counted from shapes:
+    721.4 MB eager, 385.9 MB with two fused launches, 83.9 MB compulsory, so
+    the two launches remove 52.6% of the intermediate traffic (46.5% of all of
+    it) and a single-kernel block all of it."""
+    bench = _bench()
+
+    t = bench.preset_traffic("mlp_block", 16384, 1024, 4096, 1)
+    assert round(t["eager_bytes"] / 1e6, 1) == 721.4
+    assert round(t["fused_bytes"] / 1e6, 1) == 385.9
+    assert round(t["compulsory_bytes"] / 1e6, 1) == 83.9
+    assert t["fused_eliminated"] == 0.5263 and t["fused_total_saved"] == 0.4651
+    assert t["single_kernel_eliminated"] == 1.0
+
+
+def test_preset_traffic_activation_heavy_and_stacked():
+    """The activation-heavy block adds two [M, I] round trips to eager only;
+    a stack of blocks keeps the blocks' outputs as intermediates."""
+    bench = _bench()
+
+    M, D, I = 16384, 256, 1024
+    mlp = bench.preset_traffic("mlp_block", M, D, I, 1)
+    act = bench.preset_traffic("activation_heavy", M, D, I, 1)
+    assert act["eager_bytes"] - mlp["eager_bytes"] == 2 * 2 * M * I * 2
+    assert act["fused_bytes"] == mlp["fused_bytes"] and "single_kernel_bytes" not in act
+    assert act["fused_eliminated"] > mlp["fused_eliminated"]
+    st = bench.preset_traffic("stacked_mlp", M, D, I, 4)
+    assert st["eager_bytes"] == 4 * mlp["eager_bytes"] and st["fused_bytes"] == 4 * mlp["fused_bytes"]
+    # 4 blocks: compulsory = input + 4 blocks' weights + output
+    assert st["compulsory_bytes"] == (2 * M * D + 4 * (2 * D * I + I + D)) * 2
