@@ -91,7 +91,7 @@ def _parse():
     p.add_argument("--eager-only", action="store_true",
                    help="run only the eager leg of --workload (rocprof counter runs of the eager module)")
     p.add_argument("--cpu-iters", type=int, default=5)
-    p.add_argument("--presets", default="memory_bound,medium,activation_heavy_memory_bound,"
+    p.add_argument("--presets", default="small,memory_bound,medium,activation_heavy_memory_bound,"
                    "activation_heavy_medium,stacked_memory_bound,stacked_medium",
                    help="reference presets to time ('' to skip; --configs '' skips them too)")
     p.add_argument("--settle-s", type=float, default=0.5,

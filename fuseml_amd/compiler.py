@@ -25,7 +25,8 @@ Triton/cuBLAS/bypass split) is two-way: the fused HIP kernel when the device
 is gfx950, the operands are bf16/f16 (or fp32, run as a three-term bf16 split
 product), the group fits one launch and its output
 has at least ``min_output_elements`` (the reference's tiny-output rule,
-fusion_pass.py:463 and 498: M*N < 500 000 bypasses), the GEMM is not a
+fusion_pass.py:463 and 498, M*N < 500 000 bypasses; calibrated to 0 here, see
+MIN_FUSION_OUTPUT_ELEMENTS), the GEMM is not a
 few-tile problem with a long K loop, and the epilogue saves more than the K
 loop gives up against hipBLASLt (:func:`fused_beats_eager`), else eager.  The last rule is measured on
 MI355X (bias+GELU chains against eager addmm + GELU): with K >= 2048 and fewer
@@ -52,7 +53,15 @@ from .fusion_pass import FuseMLFusionPass, fuseml_fused_kernel_placeholder, grou
 
 logger = logging.getLogger("fuseml_amd")
 
-MIN_FUSION_OUTPUT_ELEMENTS = 500_000
+# The reference bypasses groups whose output has fewer than 500 000 elements
+# (fusion_pass.py:463 and 498).  Measured on MI355X, the fused launch costs less
+# host time than the eager kernels it replaces at every size: the reference's
+# "small" preset (128 rows, 256 -> 1024 -> 256) takes 47.9 us compiled with
+# both groups fused against 62.4 us bypassed and 54.0 us eager, and fp32 C1
+# (64 rows) 77.3 against 77.6 us.  So no floor by default;
+# min_output_elements=REFERENCE_MIN_OUTPUT_ELEMENTS restores the reference's rule.
+REFERENCE_MIN_OUTPUT_ELEMENTS = 500_000
+MIN_FUSION_OUTPUT_ELEMENTS = 0
 LONG_K = 2048
 MIN_TILES_LONG_K = 256  # 128x128 output tiles; MI355X has 256 CUs
 # Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the

@@ -90,13 +90,24 @@ def test_full_pipeline_sibling_reductions(recorded):
     assert len(recorded.built) == 1 and recorded.built[0].spec.reductions == ("sum", "amax", "mean")
 
 
-def test_tiny_output_bypasses(recorded):
+def test_tiny_output_bypasses_under_the_reference_rule(recorded):
     m = TransformerMLP(64, 256).to(BF).eval()
     x = torch.randn(32, 64, dtype=BF)   # 32 x 256 < 500 000 outputs
-    be = FuseMLCompiler(require_gfx950=False)
+    be = FuseMLCompiler(require_gfx950=False, min_output_elements=comp.REFERENCE_MIN_OUTPUT_ELEMENTS)
     with torch.no_grad():
         _compile(m, be)(x)
     assert be.fusion_applied is False and recorded.built == []
+
+
+def test_tiny_output_fuses_by_default(recorded):
+    """The calibrated default has no output-size floor: a tiny group fuses."""
+    m = TransformerMLP(64, 256).to(BF).eval()
+    x = torch.randn(32, 64, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False)
+    with torch.no_grad():
+        out = _compile(m, be)(x)
+    assert torch.allclose(out.float(), m(x).float(), atol=1e-2)
+    assert be.fusion_applied and len(recorded.built) == 2
 
 
 def test_fp32_gemm_fuses_as_split_product(recorded):
@@ -169,7 +180,9 @@ def test_cost_model_rules():
     assert trigger_is_fusible(mm)[0]
     gm2 = make_fx(f)(torch.randn(16, 64, dtype=BF), torch.randn(64, 16, dtype=BF))
     mm2 = [n for n in gm2.graph.nodes if n.op == "call_function"][0]
-    assert trigger_is_fusible(mm2) == (False, "tiny output 16x16")
+    assert trigger_is_fusible(mm2)[0]  # no output-size floor by default
+    assert trigger_is_fusible(mm2, min_output_elements=comp.REFERENCE_MIN_OUTPUT_ELEMENTS) == \
+        (False, "tiny output 16x16")
     gm3 = make_fx(f)(torch.randn(1024, 60, dtype=BF), torch.randn(60, 1024, dtype=BF))
     mm3 = [n for n in gm3.graph.nodes if n.op == "call_function"][0]
     assert trigger_is_fusible(mm3)[0] is False

@@ -108,7 +108,13 @@ def test_compiled_amax_of_negated_relu():
     assert g[7] == 0.0 and np.signbit(g[7])
 
 
-def test_c1_fp32_small_is_bypassed():
+def test_c1_fp32_small_compiled():
+    """C1 (fp32, 64 rows): with the calibrated cost model its one group
+    (addmm + GELU(tanh); the second addmm has no op after it, so it is no
+    group) fuses as a split product and matches eager fp32 to 1e-4; the
+    reference's tiny-output rule (min_output_elements=500 000) bypasses it
+    instead."""
+    from fuseml_amd.compiler import REFERENCE_MIN_OUTPUT_ELEMENTS
     from fuseml_amd.workloads import c1_transformer_mlp_small
 
     wl = c1_transformer_mlp_small().to("cuda")
@@ -116,6 +122,12 @@ def test_c1_fp32_small_is_bypassed():
     with torch.no_grad():
         out = compiled(*wl.inputs)
         ref = wl.model(*wl.inputs)
+    torch.cuda.synchronize()
+    assert be.fusion_applied and be.fusion_strategy == "hip" and _launches(be) == 1
+    assert torch.allclose(out, ref, rtol=1e-4, atol=1e-4)
+    compiled, be = _compile(wl.model, min_output_elements=REFERENCE_MIN_OUTPUT_ELEMENTS)
+    with torch.no_grad():
+        out = compiled(*wl.inputs)
     assert be.fusion_applied is False
     assert torch.allclose(out, ref)
 
