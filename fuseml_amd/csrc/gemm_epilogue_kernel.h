@@ -280,6 +280,18 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Workgroup barrier that orders LDS accesses only: this wave's LDS operations
+// complete, then s_barrier.  __syncthreads() adds a release fence, which also
+// waits for every global load, store and LDS DMA this wave has in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  wait_lgkmcnt0();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
 // wherever an accumulator array is indexed, so every index is a constant and
 // the arrays stay in registers whatever the unroller decides.
@@ -457,16 +469,18 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     const int in_round = min(nwg, ntiles - round0);
     int lid = tile;
     if ((in_round & 7) == 0) lid = round0 + ((int)blockIdx.x & 7) * (in_round >> 3) + ((int)blockIdx.x >> 3);
-    // The previous tile's LDS reads and global stores are complete in every
-    // wave before this tile's DMA overwrites the slots.  The waits run on every
-    // path into the tile (on the first tile nothing is outstanding): behind a
-    // branch, the compiler's wait insertion sees the previous tile's last DMAs
-    // as possibly pending at this tile's K loop (their VGPR offsets
-    // overwritten by fragment reads there) and puts an s_waitcnt vmcnt(0) into
-    // the steady loop.
+    // The previous tile's LDS reads are complete in every wave before this
+    // tile's DMA overwrites the slots.  The waits run on every path into the
+    // tile (on the first tile nothing is outstanding).  The generic op loop's
+    // kernels of the one-wave schedules also wait for the previous tile's
+    // global stores: without that wait, the compiler's wait insertion sees
+    // them as possibly pending at this tile's K loop and puts an s_waitcnt
+    // vmcnt(0) into the steady loop.  The other kernels leave the stores in
+    // flight: their K loops' counted waits only get stricter for older
+    // operations (vector-memory operations complete in issue order).
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkmcnt0();
-    wait_vmcnt<0>();
+    if constexpr (SCHED == 3 || (SCHED == 6 && CH == kChainGeneric)) wait_vmcnt<0>();
     __builtin_amdgcn_sched_barrier(0);
     if (tile != (int)blockIdx.x) {
       asm volatile("" ::: "memory");
@@ -1576,7 +1590,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
     if (row_red) {
       // The partials overwrite the staging tile, which other waves may still be
       // draining (staged output) or reading (staged operand).
-      if (use_stage_out || staged >= 0) __syncthreads();
+      if (use_stage_out || staged >= 0) lds_barrier();
       // Row partials: the other half-wave holds the other 4-column runs of the same rows.
       static_for<0, NJ>([&](auto j) {
         const float s2 = rs[j] + __shfl_xor(rs[j], 32);
@@ -1588,7 +1602,7 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         }
       });
     }
-    __syncthreads();
+    lds_barrier();
 
     const int len = row_red ? BM : BN;
     const int nparts = row_red ? WN : WM;
