@@ -34,14 +34,18 @@ def test_algorithmic_bytes_counts_each_tensor_once():
 def test_hbm_traffic_from_committed_summaries():
     b = _bench()
     c2 = b._hbm_traffic("C2", [[16384, 4096, 1024], [16384, 1024, 4096]])
-    # the fused step writes exactly the two group outputs (h and y)
-    assert c2["fused_write_bytes"] == 16384 * 4096 * 2 + 16384 * 1024 * 2
+    # the fused step writes the two group outputs (h and y); the counters are
+    # KiB per dispatch scaled by a copy kernel's reading, so a run can be off
+    # by a few bytes
+    def near(got, want):
+        return abs(got - want) <= 1e-6 * want
+    assert near(c2["fused_write_bytes"], 16384 * 4096 * 2 + 16384 * 1024 * 2)
     assert c2["final_output_bytes"] == 16384 * 1024 * 2
     assert 0.5 < c2["intermediate_eliminated_frac"] < 0.6
     c3 = b._hbm_traffic("C3", [[16384, 4096, 1024]])
     assert c3["intermediate_eliminated_frac"] == 1.0 and c3["saved_frac"] > 0.6
     c5 = b._hbm_traffic("C5", [[8192, 16384, 4096], [8192, 4096, 16384]] * 4)
-    assert c5["fused_write_bytes"] == 4 * (8192 * 16384 * 2 + 8192 * 4096 * 2)
+    assert near(c5["fused_write_bytes"], 4 * (8192 * 16384 * 2 + 8192 * 4096 * 2))
     assert b._hbm_traffic("nope", [[1, 1, 1]]) is None
 
 
