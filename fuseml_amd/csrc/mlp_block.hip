@@ -175,6 +175,46 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Epilogue of a row block: y = acc + b2 + r as 16-bit.  acc[mb][db][r] is
+// y[m0 + 32 mb + l32][wave D/4 + 32 db + 8 (r>>2) + 4 kh + (r&3)].  No
+// branches: an absent b2 or r is a zero-length buffer (its loads read zero),
+// and rows past M are stored at an out-of-range offset (dropped).  `ln` is the
+// lane index (passed through an opaque copy by the caller).
+template <int DW, typename T>
+__device__ __forceinline__ void store_rows(const fuseml_mlp_desc& d, const f32x16_t (&acc)[2][DW], int m0, int wave,
+                                           int ln) {
+  constexpr int D = 128 * DW;
+  const int M = (int)d.M;
+  const __amdgpu_buffer_rsrc_t rb2 = make_rsrc(d.b2, d.b2 ? (int64_t)D * 2 : 0);
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(d.r ? static_cast<const char*>(d.r) + (int64_t)m0 * d.ldr * 2 : nullptr,
+                                              d.r ? ((int64_t)(M - 1 - m0) * d.ldr + D) * 2 : 0);
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<char*>(d.y) + (int64_t)m0 * d.ldy * 2,
+                                              ((int64_t)(M - 1 - m0) * d.ldy + D) * 2);
+  const int el32 = ln & 31, ekh = ln >> 5;
+  static_for<0, 2>([&](auto mb) {
+    const int ml = 32 * mb + el32;
+    const bool row_ok = m0 + ml < M;
+    static_for<0, DW>([&](auto db) {
+      static_for<0, 4>([&](auto g) {
+        const int col = wave * (D / 4) + 32 * db + 8 * g + 4 * ekh;
+        const i32x2_t b = __builtin_amdgcn_raw_buffer_load_b64(rb2, (uint32_t)col * 2u, 0, 0);
+        const i32x2_t rv = __builtin_amdgcn_raw_buffer_load_b64(
+            rr, row_ok ? ((uint32_t)ml * (uint32_t)d.ldr + (uint32_t)col) * 2u : kOOB, 0, 0);
+        float y[4];
+        static_for<0, 4>([&](auto e) {
+          const uint32_t bw = (uint32_t)(e < 2 ? b.x : b.y) >> (16 * (e & 1));
+          const uint32_t rw = (uint32_t)(e < 2 ? rv.x : rv.y) >> (16 * (e & 1));
+          y[e] = acc[mb][db][4 * g + e] + to_f32<T>(bw & 0xffffu) + to_f32<T>(rw & 0xffffu);
+        });
+        const i32x2_t out = {(int)pack2<T>(y[0], y[1]), (int)pack2<T>(y[2], y[3])};
+        __builtin_amdgcn_raw_buffer_store_b64(out, ry,
+                                              row_ok ? ((uint32_t)ml * (uint32_t)d.ldy + (uint32_t)col) * 2u : kOOB,
+                                              0, 0);
+      });
+    });
+  });
+}
+
 // DW: 32-column blocks of y per wave (D = 128 DW).  GELU: FUSEML_OP_GELU_ERF or _TANH.
 template <int DW, int GELU, typename T>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1)))
@@ -330,37 +370,176 @@ void mlp_block_kernel(const fuseml_mlp_desc d) {
       });
     }
 
-    // Epilogue: y = acc + b2 + r, 16-bit.  acc[mb][db][r] is
-    // y[m0 + 32 mb + l32][wave D/4 + 32 db + 8 (r>>2) + 4 kh + (r&3)].  No
-    // branches: an absent b2 or r is a zero-length buffer (its loads read zero),
-    // and rows past M are stored at an out-of-range offset (dropped).
-    const __amdgpu_buffer_rsrc_t rb2 = make_rsrc(d.b2, d.b2 ? (int64_t)D * 2 : 0);
-    const __amdgpu_buffer_rsrc_t rr = make_rsrc(d.r ? static_cast<const char*>(d.r) + (int64_t)m0 * d.ldr * 2 : nullptr,
-                                                d.r ? ((int64_t)(M - 1 - m0) * d.ldr + D) * 2 : 0);
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<char*>(d.y) + (int64_t)m0 * d.ldy * 2,
-                                                ((int64_t)(M - 1 - m0) * d.ldy + D) * 2);
-    const int el32 = ln & 31, ekh = ln >> 5;
+    store_rows<DW, T>(d, acc, m0, wave, ln);
+  }
+}
+
+// The block with I split across the waves instead of D (I a multiple of
+// 128): super-chunk c holds intermediate columns [128 c, 128 c + 128), and wave
+// w computes h[64, 32] for its own 32 of them over the whole of D (GEMM1: no
+// partials to combine), adds b1, applies GELU and writes its h columns as
+// 16-bit into an LDS h tile; after one barrier every wave multiplies the whole
+// h[64, 128] by its D/4 rows of W2 into its y accumulators (GEMM2).  The h
+// tile is double-buffered, so one barrier per super-chunk suffices: a wave
+// writing h(c + 1) has passed the barrier of c, which every wave reached after
+// its GEMM2 of c - 1.
+//   * Weight fragments stream from global memory (the weights stay in L2) in
+//     consumption order, W1's D/16 fragments then W2's 8 x DW, through a ring
+//     of kRing registers sets: fragment f is loaded when fragment f - kRing is
+//     consumed (across super-chunk boundaries).
+//   * h tile [64][128] 16-bit, 256-byte rows: logical 16-byte chunk q of row m
+//     at chunk q ^ (m & 15), its 8-byte halves exchanged when bit 4 of m is
+//     set, so that a GEMM1 write (32 rows, one half each) and a GEMM2 fragment
+//     read (16 rows per bank sweep) are free of bank conflicts.
+constexpr int kIC = 128;                   // intermediate columns per super-chunk
+constexpr int kHBytes = kBM * kIC * 2;     // one h tile
+constexpr int kRing = 16;                  // weight fragments in flight per wave
+
+__device__ __forceinline__ int h_chunk(int m, int q) { return m * (kIC * 2) + ((q ^ (m & 15)) << 4); }
+__device__ __forceinline__ int h_byte(int m, int q, int half) { return h_chunk(m, q) + ((half ^ ((m >> 4) & 1)) << 3); }
+
+template <int DW, int GELU, typename T>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1)))
+void mlp_block_kernel_isplit(const fuseml_mlp_desc d) {
+  constexpr int D = 128 * DW;
+  constexpr int PITCH = 2 * D;
+  constexpr int NF1 = D / 16;        // W1 fragments (GEMM1 k-steps) per super-chunk
+  constexpr int KS2 = kIC / 16;      // GEMM2 k-steps
+  constexpr int NF = NF1 + KS2 * DW; // weight fragments per super-chunk
+  static_assert(NF % kRing == 0, "a super-chunk consumes whole ring turns");
+  __shared__ __attribute__((aligned(1024))) char smem[kBM * PITCH + 2 * kHBytes];
+  char* xs = smem;
+  char* hs = smem + kBM * PITCH;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int kh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = (int)d.M, I = (int)d.I;
+  const int nblocks = (M + kBM - 1) / kBM;
+  const int nsc = I / kIC;
+
+  const __amdgpu_buffer_rsrc_t rw1 = make_rsrc(d.w1, ((int64_t)(I - 1) * d.ldw1 + D) * 2);
+  const __amdgpu_buffer_rsrc_t rw2 = make_rsrc(d.w2, ((int64_t)(D - 1) * d.ldw2 + I) * 2);
+  const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(d.b1, (int64_t)I * 2);
+
+  // Fragment f of super-chunk c.  W1 (f < NF1, k-step s = f): row
+  // i = 128 c + 32 wave + l32, columns [16 s + 8 kh, +8).  W2 (f = NF1 +
+  // DW s + db): row wave D/4 + 32 db + l32, columns [128 c + 16 s + 8 kh, +8).
+  const uint32_t w1_lane = ((uint32_t)(32 * wave + l32) * (uint32_t)d.ldw1 + (uint32_t)(8 * kh)) * 2u;
+  const uint32_t w1_sc = (uint32_t)kIC * (uint32_t)d.ldw1 * 2u;
+  const uint32_t w2_lane = ((uint32_t)(wave * (D / 4) + l32) * (uint32_t)d.ldw2 + (uint32_t)(8 * kh)) * 2u;
+  const uint32_t w2_dblk = 32u * (uint32_t)d.ldw2 * 2u;
+  auto frag = [&](int c, auto f) -> i32x4_t {
+    constexpr int F = decltype(f)::value;
+    if constexpr (F < NF1) {
+      return __builtin_amdgcn_raw_buffer_load_b128(rw1, w1_lane + (uint32_t)c * w1_sc + (uint32_t)(32 * F), 0, 0);
+    } else {
+      constexpr int s = (F - NF1) / DW, db = (F - NF1) % DW;
+      return __builtin_amdgcn_raw_buffer_load_b128(
+          rw2, w2_lane + (uint32_t)db * w2_dblk + (uint32_t)(c * kIC * 2 + 32 * s), 0, 0);
+    }
+  };
+  i32x4_t ring[kRing];
+  // Before consuming fragment F of super-chunk c: load fragment F + kRing
+  // (of c, or of c + 1 past the end; nothing past the last super-chunk).
+  auto refill = [&](int c, auto f) {
+    constexpr int F = decltype(f)::value;
+    constexpr int G = F + kRing;
+    if constexpr (G < NF) {
+      ring[G % kRing] = frag(c, std::integral_constant<int, G>{});
+    } else {
+      if (c + 1 < nsc) ring[G % kRing] = frag(c + 1, std::integral_constant<int, G - NF>{});
+    }
+  };
+
+  for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
+    const int m0 = blk * kBM;
+    if (blk != (int)blockIdx.x) barrier();  // the previous block no longer reads x
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    {
+      const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(d.x) + (int64_t)m0 * d.ldx * 2,
+                                                  ((int64_t)(M - 1 - m0) * d.ldx + D) * 2);
+      constexpr int kDmas = kBM * PITCH / 1024;
+      for (int i = wave; i < kDmas; i += 4) {
+        const int byte = i * 1024 + ln * 16;
+        const int m = byte / PITCH;
+        const int p = (byte % PITCH) >> 4;
+        const int q = p ^ (m & 15);
+        const uint32_t off = m0 + m < M ? ((uint32_t)m * (uint32_t)d.ldx + (uint32_t)(8 * q)) * 2u : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + i * 1024),
+                                                 16, off, 0, 0, 0);
+      }
+    }
+    static_for<0, kRing>([&](auto f) {
+      if constexpr (decltype(f)::value < NF) ring[f] = frag(0, f);
+    });
+    f32x16_t acc[2][DW];
     static_for<0, 2>([&](auto mb) {
-      const int ml = 32 * mb + el32;
-      const bool row_ok = m0 + ml < M;
       static_for<0, DW>([&](auto db) {
-        static_for<0, 4>([&](auto g) {
-          const int col = wave * (D / 4) + 32 * db + 8 * g + 4 * ekh;
-          const i32x2_t b = __builtin_amdgcn_raw_buffer_load_b64(rb2, (uint32_t)col * 2u, 0, 0);
-          const i32x2_t rv = __builtin_amdgcn_raw_buffer_load_b64(
-              rr, row_ok ? ((uint32_t)ml * (uint32_t)d.ldr + (uint32_t)col) * 2u : kOOB, 0, 0);
-          float y[4];
-          static_for<0, 4>([&](auto e) {
-            const uint32_t bw = (uint32_t)(e < 2 ? b.x : b.y) >> (16 * (e & 1));
-            const uint32_t rw = (uint32_t)(e < 2 ? rv.x : rv.y) >> (16 * (e & 1));
-            y[e] = acc[mb][db][4 * g + e] + to_f32<T>(bw & 0xffffu) + to_f32<T>(rw & 0xffffu);
-          });
-          const i32x2_t out = {(int)pack2<T>(y[0], y[1]), (int)pack2<T>(y[2], y[3])};
-          __builtin_amdgcn_raw_buffer_store_b64(
-              out, ry, row_ok ? ((uint32_t)ml * (uint32_t)d.ldy + (uint32_t)col) * 2u : kOOB, 0, 0);
-        });
+        static_for<0, 16>([&](auto r) { acc[mb][db][(int)r] = 0.0f; });
       });
     });
+    wait_vmcnt0();
+    barrier();  // x tile landed
+
+    for (int c = 0; c < nsc; ++c) {
+      // b1 for this lane's 16 h columns: 128 c + 32 wave + 8 g + 4 kh + e.
+      i32x2_t bq[4];
+      static_for<0, 4>([&](auto g) {
+        bq[g] = __builtin_amdgcn_raw_buffer_load_b64(rb1, (uint32_t)(c * kIC + 32 * wave + 8 * g + 4 * kh) * 2u, 0, 0);
+      });
+      // GEMM1: h[64, this wave's 32 columns] over all of D.
+      f32x16_t h1[2];
+      static_for<0, 2>([&](auto mb) { static_for<0, 16>([&](auto r) { h1[mb][(int)r] = 0.0f; }); });
+      static_for<0, NF1>([&](auto s) {
+        const i32x4_t w = ring[s % kRing];
+        refill(c, s);
+        static_for<0, 2>([&](auto mb) {
+          const int m = 32 * mb + l32;
+          const i32x4_t xf = *reinterpret_cast<const i32x4_t*>(xs + x_chunk(m, 2 * s + kh, PITCH));
+          h1[mb] = mfma32<T>(w, xf, h1[mb]);
+        });
+      });
+      // h1[mb][r] = h[32 mb + l32][32 wave + 8 (r>>2) + 4 kh + (r&3)]: + b1, GELU, 16-bit into h(c % 2).
+      char* hb = hs + (c & 1) * kHBytes;
+      static_for<0, 2>([&](auto mb) {
+        const int m = 32 * mb + l32;
+        static_for<0, 4>([&](auto g) {
+          float v[4];
+          static_for<0, 4>([&](auto e) {
+            const uint32_t bw = (uint32_t)(e < 2 ? bq[g].x : bq[g].y) >> (16 * (e & 1));
+            v[e] = h1[mb][4 * g + e] + to_f32<T>(bw & 0xffffu);
+            if constexpr (GELU == FUSEML_OP_GELU_TANH)
+              v[e] = gelu_tanh(v[e]);
+            else
+              v[e] = gelu_erf(v[e]);
+          });
+          const i32x2_t hv = {(int)pack2<T>(v[0], v[1]), (int)pack2<T>(v[2], v[3])};
+          *reinterpret_cast<i32x2_t*>(hb + h_byte(m, 4 * wave + g, kh)) = hv;
+        });
+      });
+      barrier();  // h(c) complete
+      // GEMM2: y[64, this wave's D/4 columns] += h[64, 128] W2[rows, 128 c .. 128 c + 128]^T.
+      static_for<0, KS2>([&](auto s) {
+        i32x4_t hf[2];
+        static_for<0, 2>([&](auto mb) {
+          const int m = 32 * mb + l32;
+          i32x4_t x = *reinterpret_cast<const i32x4_t*>(hb + h_chunk(m, 2 * s + kh));
+          if ((m >> 4) & 1) x = i32x4_t{x.z, x.w, x.x, x.y};
+          hf[mb] = x;
+        });
+        static_for<0, DW>([&](auto db) {
+          constexpr int F = NF1 + DW * decltype(s)::value + decltype(db)::value;
+          const i32x4_t w = ring[F % kRing];
+          refill(c, std::integral_constant<int, F>{});
+          static_for<0, 2>([&](auto mb) { acc[mb][db] = mfma32<T>(w, hf[mb], acc[mb][db]); });
+        });
+      });
+    }
+    store_rows<DW, T>(d, acc, m0, wave, ln);
   }
 }
 
@@ -434,12 +613,36 @@ int validate(const fuseml_mlp_desc* dp) {
   return FUSEML_OK;
 }
 
+// Which kernel runs a descriptor: the I-split one when I is a multiple of its
+// 128-column super-chunk (FUSEML_MLP_KERNEL=dsplit forces the other, for A/B
+// measurements; read once per process).
+bool use_isplit(const fuseml_mlp_desc& d) {
+  static const bool force_dsplit = [] {
+    const char* e = getenv("FUSEML_MLP_KERNEL");
+    return e != nullptr && strcmp(e, "dsplit") == 0;
+  }();
+  return d.I % kIC == 0 && d.D <= 512 && !force_dsplit;
+}
+
 template <int DW, typename T>
 hipError_t launch_dw(const fuseml_mlp_desc& d, int grid, hipStream_t s) {
-  if (d.gelu == FUSEML_OP_GELU_TANH)
+  const bool tanh_gelu = d.gelu == FUSEML_OP_GELU_TANH;
+  // D = 1024 stays on the D-split kernel: the I-split one's 64 x 1024
+  // accumulators and weight ring do not fit the register file.
+  if constexpr (DW <= 4) {
+    if (use_isplit(d)) {
+      if (tanh_gelu)
+        hipLaunchKernelGGL((mlp_block_kernel_isplit<DW, FUSEML_OP_GELU_TANH, T>), dim3(grid), dim3(kThreads), 0, s, d);
+      else
+        hipLaunchKernelGGL((mlp_block_kernel_isplit<DW, FUSEML_OP_GELU_ERF, T>), dim3(grid), dim3(kThreads), 0, s, d);
+      return hipGetLastError();
+    }
+  }
+  if (tanh_gelu) {
     hipLaunchKernelGGL((mlp_block_kernel<DW, FUSEML_OP_GELU_TANH, T>), dim3(grid), dim3(kThreads), 0, s, d);
-  else
+  } else {
     hipLaunchKernelGGL((mlp_block_kernel<DW, FUSEML_OP_GELU_ERF, T>), dim3(grid), dim3(kThreads), 0, s, d);
+  }
   return hipGetLastError();
 }
 
