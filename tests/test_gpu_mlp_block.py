@@ -7,6 +7,8 @@ path (and eager bf16) do.  Cases: every supported width D (256, 512, 1024),
 ragged M (not a multiple of the 64-row block), I down to one 32-column chunk,
 GELU erf and tanh, bf16 and fp16, no bias/residual, and the C2 config at full
 size through the launcher and through ``FuseMLCompiler(fuse_mlp_block=True)``.
+The shapes run both kernels: the I-split one (D of 256 or 512 and I a multiple
+of 128) and the D-split one (D = 1024 or I not a multiple of 128).
 
 Tolerance: ``allclose(rtol=2e-2, atol=2e-2)`` against the float64 oracle.
 """
@@ -53,7 +55,8 @@ def _oracle(x, w1, b1, w2, b2, r, approximate="none", dtype=None):
 
 
 @pytest.mark.parametrize("approximate", ["none", "tanh"])
-@pytest.mark.parametrize("shape", [(300, 256, 1024), (129, 512, 96), (64, 1024, 32), (1, 256, 64), (200, 1024, 2048)],
+@pytest.mark.parametrize("shape", [(300, 256, 1024), (129, 512, 96), (64, 1024, 32), (1, 256, 64), (200, 1024, 2048),
+                                   (129, 512, 384), (1, 256, 128), (65, 256, 1152), (640, 512, 2048)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_mlp_block_parity(shape, approximate):
     from fuseml_amd.mlp import HipMlpLauncher
