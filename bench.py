@@ -470,8 +470,9 @@ def _presets(args, dev):
 
             res["eager"] = _time_sync(lambda: m(x), args)
             res["eager"]["check"] = gate(m(x))
+            # all_fused: every group as its own launch (no single-kernel MLP)
             paths = {"compiled": {}, "all_fused": dict(k_per_epilogue_pass=0, min_tiles_long_k=0,
-                                                       min_output_elements=0)}
+                                                       min_output_elements=0, fuse_mlp_block=False)}
             if kind != "activation_heavy":
                 paths["single_kernel_mlp"] = dict(fuse_mlp_block=True, k_per_epilogue_pass=0, min_tiles_long_k=0,
                                                   min_output_elements=0)
@@ -488,8 +489,7 @@ def _presets(args, dev):
                 r.update(check=gate(y), fusion_strategy=be.fusion_strategy,
                          fused_launchers=len({id(L) for L in be.launchers}), dispatch=be.dispatch[:1],
                          speedup_vs_eager=round(res["eager"]["median_ms"] / r["median_ms"], 3))
-                if label == "single_kernel_mlp":
-                    r["single_kernel_launchers"] = n_mlp
+                r["single_kernel_launchers"] = n_mlp
                 res[label] = r
         out[name] = res
         del wl, m, x, ref

@@ -17,7 +17,7 @@ import os
 import threading
 from typing import Optional
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_OPS = 16
 MAX_OPERANDS = 8
 MAX_EXTRA_OUT = 4
@@ -83,6 +83,8 @@ EXPORTED_SYMBOLS = (
     "fuseml_mfma_peak_probe",
     "fuseml_mlp_block",
     "fuseml_mlp_block_supported",
+    "fuseml_mlp_pack_bytes",
+    "fuseml_mlp_pack_weights",
     "fuseml_split_bf16x3",
 )
 
@@ -160,6 +162,7 @@ class MlpDesc(ctypes.Structure):
         ("ldy", ctypes.c_int64),
         ("dtype", ctypes.c_int32),
         ("gelu", ctypes.c_int32),
+        ("wpack", ctypes.c_void_p),
     ]
 
 
@@ -204,6 +207,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fuseml_mlp_block.restype = ctypes.c_int
     lib.fuseml_mlp_block_supported.argtypes = [mlp_p]
     lib.fuseml_mlp_block_supported.restype = ctypes.c_int
+    lib.fuseml_mlp_pack_bytes.argtypes = [mlp_p]
+    lib.fuseml_mlp_pack_bytes.restype = ctypes.c_int64
+    lib.fuseml_mlp_pack_weights.argtypes = [mlp_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.fuseml_mlp_pack_weights.restype = ctypes.c_int
     lib.fuseml_desc_size.argtypes = []
     lib.fuseml_desc_size.restype = ctypes.c_size_t
     lib.fuseml_mlp_desc_size.argtypes = []

@@ -1,6 +1,7 @@
 """The measurement behind the cost model's two thresholds (fused kernel or eager).
 
     python -m fuseml_amd.calibration [--out profiles/cost_model_calibration.json]
+    python -m fuseml_amd.calibration --mlp [--out profiles/mlp_block_crossover.json]
 
 For each group below, on one GPU, the same inputs run three ways:
 
@@ -66,6 +67,15 @@ FEW_TILES: List[Tuple[str, str, int, int, int]] = [
     for k in (1024, 2048, 4096, 8192)
 ]
 GROUPS = CONFIG_GROUPS + K_SWEEP + FEW_TILES
+
+# (M, D, I) MLP blocks (linear2(gelu(linear1(x))) + x) for the single-kernel
+# MLP's rule (``--mlp``): the reference's memory-bound widths over M, and C2.
+MLP_SWEEP: List[Tuple[int, int, int]] = (
+    [(M, 256, 1024) for M in (2048, 4096, 8192, 16384, 32768, 65536)]
+    + [(M, 256, 4096) for M in (4096, 8192, 16384, 32768)]
+    + [(M, 512, 2048) for M in (8192, 16384, 32768)]
+    + [(16384, 1024, 4096)]
+)
 
 
 def _spec(chain: str):
@@ -166,20 +176,86 @@ def measure(groups=GROUPS, passes: int = 2, dev: str = "cuda") -> List[Dict[str,
     return rows
 
 
+def _reference_ms(fn: Callable[[], object], iters: int) -> float:
+    """The reference harness's timing: events around one call, a
+    synchronisation after each, median."""
+    for _ in range(10):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return statistics.median(ts)
+
+
+def measure_mlp(shapes=MLP_SWEEP, passes: int = 2, dev: str = "cuda") -> List[Dict[str, object]]:
+    """Per MLP block shape: the compiled module with two launches (the default
+    cost model, no single kernel) and with the single-kernel MLP, timed the
+    reference's way; best of alternating passes."""
+    from .compiler import FuseMLCompiler
+    from .mlp import HipMlpLauncher, mlp_block_beats_two_launches
+    from .workloads import TransformerMLP
+
+    rows = []
+    for M, D, I in shapes:
+        torch.manual_seed(0)
+        model = TransformerMLP(D, I).to(dev, BF).eval()
+        x = torch.randn(M, D, device=dev, dtype=BF)
+        fns = {}
+        with torch.no_grad():
+            for label, kw in (("two", dict(fuse_mlp_block=False)),
+                              ("single", dict(fuse_mlp_block=True, k_per_epilogue_pass=0, min_tiles_long_k=0,
+                                              min_output_elements=0))):
+                torch._dynamo.reset()
+                be = FuseMLCompiler(**kw)
+                c = torch.compile(model, backend=be)
+                c(x)
+                if label == "single" and not any(isinstance(L, HipMlpLauncher) for L in be.launchers):
+                    raise RuntimeError(f"M={M} D={D} I={I}: the single-kernel MLP did not bind")
+                fns[label] = c
+            iters = max(50, min(300, int(3e10 / (4.0 * M * D * I) * 50)))
+            best = {k: float("inf") for k in fns}
+            for _ in range(passes):
+                for k, f in fns.items():
+                    best[k] = min(best[k], _reference_ms(lambda: f(x), iters))
+        rows.append({"M": M, "D": D, "I": I, "two_ms": round(best["two"], 4), "single_ms": round(best["single"], 4),
+                     "single_over_two": round(best["single"] / best["two"], 3),
+                     "rule_binds": bool(mlp_block_beats_two_launches(M, D, I)[0])})
+        print(f"[calibration] mlp M={M} D={D} I={I}: two {best['two']:.4f} single {best['single']:.4f} ms",
+              file=sys.stderr, flush=True)
+        del fns, model, x
+        torch._dynamo.reset()
+        torch.cuda.empty_cache()
+    return rows
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--out", default="", help="write the JSON here (default: stdout)")
     ap.add_argument("--passes", type=int, default=2)
+    ap.add_argument("--mlp", action="store_true",
+                    help="measure the single-kernel MLP against two launches (MLP_SWEEP) instead of the GEMM groups")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("calibration needs a GPU", file=sys.stderr)
         return 2
     t0 = time.perf_counter()
-    rows = measure(passes=args.passes)
+    if args.mlp:
+        rows = measure_mlp(passes=args.passes)
+        method = ("compiled TransformerMLP (bf16), events around one forward and a synchronisation after each "
+                  "(the reference harness's method), median, best of alternating passes; two = default cost model "
+                  "without the single kernel, single = the single-kernel MLP bound")
+    else:
+        rows = measure(passes=args.passes)
+        method = "median HIP-event time per call, best of alternating passes; same inputs for all three paths"
     arch = getattr(torch.cuda.get_device_properties(0), "gcnArchName", "")
-    doc = {"device": arch, "seconds": round(time.perf_counter() - t0, 1),
-           "method": "median HIP-event time per call, best of alternating passes; same inputs for all three paths",
-           "rows": rows}
+    doc = {"device": arch, "cus": torch.cuda.get_device_properties(0).multi_processor_count,
+           "seconds": round(time.perf_counter() - t0, 1), "method": method, "rows": rows}
     text = json.dumps(doc, indent=1)
     if args.out:
         with open(args.out, "w") as f:

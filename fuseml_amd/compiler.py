@@ -40,7 +40,7 @@ wins at every size (1.2-1.36x below 256 tiles).
 from __future__ import annotations
 
 import logging
-from typing import Any, Callable, Dict, List, Optional, Tuple
+from typing import Any, Callable, Dict, List, Optional, Tuple, Union
 
 import torch
 import torch.fx
@@ -339,7 +339,7 @@ class FuseMLCompiler:
     """``torch.compile`` backend fusing addmm/mm epilogue chains into HIP kernels."""
 
     def __init__(self, registry: Any = None, *, fuse_sibling_reductions: bool = False,
-                 fuse_leading_views: bool = False, fuse_mlp_block: bool = False,
+                 fuse_leading_views: bool = False, fuse_mlp_block: Union[bool, str] = "auto",
                  min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
                  min_tiles_long_k: int = MIN_TILES_LONG_K,
                  k_per_epilogue_pass: int = K_PER_EPILOGUE_PASS,
@@ -353,6 +353,8 @@ class FuseMLCompiler:
         self.dispatch: List[str] = []
         self.fuse_sibling_reductions = fuse_sibling_reductions
         self.fuse_leading_views = fuse_leading_views
+        if fuse_mlp_block not in (True, False, "auto"):
+            raise ValueError(f"fuse_mlp_block must be True, False or 'auto', not {fuse_mlp_block!r}")
         self.fuse_mlp_block = fuse_mlp_block
         self.min_output_elements = min_output_elements
         self.min_tiles_long_k = min_tiles_long_k
@@ -490,8 +492,10 @@ class FuseMLCompiler:
                          strategies: set) -> List[torch.fx.Node]:
         """Bind each (GEMM1+bias+GELU, GEMM2+bias+residual) placeholder pair whose
         GELU output feeds only the second GEMM to one single-kernel MLP launcher
-        (``fuse_mlp_block=True``); return the placeholders left to bind."""
-        from .mlp import HipMlpLauncher, mlp_eager_fn, mlp_first_group, mlp_second_group, mlp_shape_supported
+        (``fuse_mlp_block=True``, or ``"auto"`` where the single kernel measured
+        faster); return the placeholders left to bind."""
+        from .mlp import (HipMlpLauncher, mlp_block_beats_two_launches, mlp_eager_fn, mlp_first_group,
+                          mlp_second_group, mlp_shape_supported)
 
         specs: Dict[torch.fx.Node, Any] = {}
         for ph in placeholders:
@@ -512,12 +516,15 @@ class FuseMLCompiler:
             if m1 is None or list(ph1.users) != [ph2]:
                 continue
             g1, g2 = ph1.meta["fusion_group"], ph2.meta["fusion_group"]
-            # both GEMMs must pass the pre-scan's cost model (tiny outputs and
-            # few-tile long-K GEMMs stay eager whichever kernel would run them)
-            verdicts = [g.base_node.meta.get("fuseml_cost_model") for g in (g1, g2)]
-            if verdicts != ["fused", "fused"]:
-                logger.info("MLP pair %s + %s stays unbound: %s", g1, g2, verdicts)
-                continue
+            if self.fuse_mlp_block is True:
+                # forced: both GEMMs must still pass the pre-scan's cost model
+                # (tiny outputs and few-tile long-K GEMMs stay eager whichever
+                # kernel would run them); "auto" applies its measured rule below,
+                # which compares the single kernel with the default path
+                verdicts = [g.base_node.meta.get("fuseml_cost_model") for g in (g1, g2)]
+                if verdicts != ["fused", "fused"]:
+                    logger.info("MLP pair %s + %s stays unbound: %s", g1, g2, verdicts)
+                    continue
             n1, n2 = len(g1.inputs), len(g2.inputs)
             slots1 = {k: m1[k] for k in ("x", "w1t", "b1")}
             slots2 = {k: m2[k] for k in ("h", "w2t", "b2", "r")}
@@ -526,7 +533,10 @@ class FuseMLCompiler:
             xm, wm, dt = _meta(ph1.args[m1["x"]]), _meta(ph1.args[m1["w1t"]]), specs[ph1].out_dtype
             if xm is None or wm is None or len(xm.shape) != 2 or len(wm.shape) != 2:
                 continue
-            ok, why = mlp_shape_supported(int(xm.shape[0]), int(xm.shape[1]), int(wm.shape[1]), dt)
+            M, D, I = int(xm.shape[0]), int(xm.shape[1]), int(wm.shape[1])
+            ok, why = mlp_shape_supported(M, D, I, dt)
+            if ok and self.fuse_mlp_block == "auto":
+                ok, why = mlp_block_beats_two_launches(M, D, I)
             if not ok:
                 logger.info("MLP pair %s + %s keeps two launches: %s", g1, g2, why)
                 continue

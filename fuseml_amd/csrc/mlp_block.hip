@@ -398,7 +398,9 @@ constexpr int kRing = 16;                  // weight fragments in flight per wav
 __device__ __forceinline__ int h_chunk(int m, int q) { return m * (kIC * 2) + ((q ^ (m & 15)) << 4); }
 __device__ __forceinline__ int h_byte(int m, int q, int half) { return h_chunk(m, q) + ((half ^ ((m >> 4) & 1)) << 3); }
 
-template <int DW, int GELU, typename T>
+// PACK: the weight fragments come from d.wpack (fuseml_mlp_pack_weights), one
+// contiguous 1 KB block per fragment, instead of from W1 and W2.
+template <int DW, int GELU, typename T, bool PACK>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1)))
 void mlp_block_kernel_isplit(const fuseml_mlp_desc d) {
   constexpr int D = 128 * DW;
@@ -431,9 +433,13 @@ void mlp_block_kernel_isplit(const fuseml_mlp_desc d) {
   const uint32_t w1_sc = (uint32_t)kIC * (uint32_t)d.ldw1 * 2u;
   const uint32_t w2_lane = ((uint32_t)(wave * (D / 4) + l32) * (uint32_t)d.ldw2 + (uint32_t)(8 * kh)) * 2u;
   const uint32_t w2_dblk = 32u * (uint32_t)d.ldw2 * 2u;
+  const __amdgpu_buffer_rsrc_t rwp = make_rsrc(d.wpack, PACK ? (int64_t)4 * D * I : 0);
+  const uint32_t wp_lane = (uint32_t)(wave * NF * 1024 + lane * 16);
   auto frag = [&](int c, auto f) -> i32x4_t {
     constexpr int F = decltype(f)::value;
-    if constexpr (F < NF1) {
+    if constexpr (PACK) {
+      return __builtin_amdgcn_raw_buffer_load_b128(rwp, wp_lane + (uint32_t)(c * 4 * NF * 1024 + F * 1024), 0, 0);
+    } else if constexpr (F < NF1) {
       return __builtin_amdgcn_raw_buffer_load_b128(rw1, w1_lane + (uint32_t)c * w1_sc + (uint32_t)(32 * F), 0, 0);
     } else {
       constexpr int s = (F - NF1) / DW, db = (F - NF1) % DW;
@@ -543,6 +549,30 @@ void mlp_block_kernel_isplit(const fuseml_mlp_desc d) {
   }
 }
 
+// fuseml_mlp_pack_weights: block b of the packed buffer is fragment f of wave w
+// of super-chunk c (b = (4 c + w) NF + f, NF = D/8 fragments per wave and
+// super-chunk, in the I-split kernel's consumption order); lane l writes its
+// 16 bytes at b * 1024 + 16 l.  One wave per block.
+__global__ __launch_bounds__(64) void mlp_pack_kernel(const fuseml_mlp_desc d, char* wpack) {
+  const int D = (int)d.D;
+  const int DW = D / 128;
+  const int NF1 = D / 16;
+  const int NF = D / 8;
+  const int b = blockIdx.x;
+  const int c = b / (4 * NF), w = (b / NF) % 4, f = b % NF;
+  const int l32 = threadIdx.x & 31, kh = threadIdx.x >> 5;
+  const uint16_t* src;
+  if (f < NF1) {
+    const int row = kIC * c + 32 * w + l32;
+    src = static_cast<const uint16_t*>(d.w1) + (int64_t)row * d.ldw1 + 16 * f + 8 * kh;
+  } else {
+    const int s = (f - NF1) / DW, db = (f - NF1) % DW;
+    const int row = w * (D / 4) + 32 * db + l32;
+    src = static_cast<const uint16_t*>(d.w2) + (int64_t)row * d.ldw2 + kIC * c + 16 * s + 8 * kh;
+  }
+  *reinterpret_cast<i32x4_t*>(wpack + (int64_t)b * 1024 + threadIdx.x * 16) = *reinterpret_cast<const i32x4_t*>(src);
+}
+
 void set_error(const char* msg) { fuseml_detail::set_error_text(msg); }
 
 // gfx950 check and CU count, queried once per device.
@@ -603,6 +633,10 @@ int validate(const fuseml_mlp_desc* dp) {
     set_error("mlp_block: strides or alignment not supported");
     return FUSEML_EUNSUPPORTED;
   }
+  if (d.wpack != nullptr && (((uintptr_t)d.wpack & 15) || (int64_t)4 * d.D * d.I >= ((int64_t)1 << 31))) {
+    set_error("mlp_block: packed weights misaligned or 2 GiB or more");
+    return FUSEML_EUNSUPPORTED;
+  }
   // 32-bit buffer offsets: the weights are addressed whole, x and r per row block.
   const int64_t lim = (int64_t)1 << 31;
   if (((d.I - 1) * d.ldw1 + d.D) * 2 >= lim || ((d.D - 1) * d.ldw2 + d.I) * 2 >= lim ||
@@ -631,10 +665,15 @@ hipError_t launch_dw(const fuseml_mlp_desc& d, int grid, hipStream_t s) {
   // accumulators and weight ring do not fit the register file.
   if constexpr (DW <= 4) {
     if (use_isplit(d)) {
-      if (tanh_gelu)
-        hipLaunchKernelGGL((mlp_block_kernel_isplit<DW, FUSEML_OP_GELU_TANH, T>), dim3(grid), dim3(kThreads), 0, s, d);
+      const bool pack = d.wpack != nullptr;
+      if (tanh_gelu && pack)
+        hipLaunchKernelGGL((mlp_block_kernel_isplit<DW, FUSEML_OP_GELU_TANH, T, true>), dim3(grid), dim3(kThreads), 0, s, d);
+      else if (tanh_gelu)
+        hipLaunchKernelGGL((mlp_block_kernel_isplit<DW, FUSEML_OP_GELU_TANH, T, false>), dim3(grid), dim3(kThreads), 0, s, d);
+      else if (pack)
+        hipLaunchKernelGGL((mlp_block_kernel_isplit<DW, FUSEML_OP_GELU_ERF, T, true>), dim3(grid), dim3(kThreads), 0, s, d);
       else
-        hipLaunchKernelGGL((mlp_block_kernel_isplit<DW, FUSEML_OP_GELU_ERF, T>), dim3(grid), dim3(kThreads), 0, s, d);
+        hipLaunchKernelGGL((mlp_block_kernel_isplit<DW, FUSEML_OP_GELU_ERF, T, false>), dim3(grid), dim3(kThreads), 0, s, d);
       return hipGetLastError();
     }
   }
@@ -662,6 +701,42 @@ extern "C" {
 int fuseml_mlp_block_supported(const fuseml_mlp_desc* desc) {
   set_error("");
   return validate(desc) == FUSEML_OK ? 1 : 0;
+}
+
+int64_t fuseml_mlp_pack_bytes(const fuseml_mlp_desc* desc) {
+  set_error("");
+  if (validate(desc) != FUSEML_OK) return 0;
+  if (!(desc->D == 256 || desc->D == 512) || desc->I % kIC != 0) return 0;
+  return (int64_t)4 * desc->D * desc->I;
+}
+
+int fuseml_mlp_pack_weights(const fuseml_mlp_desc* desc, void* wpack, void* stream) {
+  set_error("");
+  const int rc = validate(desc);
+  if (rc != FUSEML_OK) return rc;
+  if (!(desc->D == 256 || desc->D == 512) || desc->I % kIC != 0) {
+    set_error("mlp_pack_weights: D must be 256 or 512 and I a multiple of 128");
+    return FUSEML_EUNSUPPORTED;
+  }
+  if (wpack == nullptr || ((uintptr_t)wpack & 15)) {
+    set_error("mlp_pack_weights: destination missing or not 16-byte aligned");
+    return FUSEML_EINVAL;
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("hipGetDevice failed");
+    return FUSEML_EHIP;
+  }
+  const int cus = device_cus(dev);
+  if (cus <= 0) return cus < 0 ? cus : FUSEML_EHIP;
+  const int64_t blocks = (desc->I / kIC) * 4 * (desc->D / 8);
+  hipLaunchKernelGGL(mlp_pack_kernel, dim3((unsigned)blocks), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), *desc,
+                     static_cast<char*>(wpack));
+  if (hipGetLastError() != hipSuccess) {
+    set_error("mlp_pack_weights launch failed");
+    return FUSEML_EHIP;
+  }
+  return FUSEML_OK;
 }
 
 int fuseml_mlp_block(const fuseml_mlp_desc* desc, void* stream) {

@@ -12,7 +12,9 @@ is written to HBM by the first launch and read back by the second.  With
 is bound to one :class:`HipMlpLauncher`, which calls ``fuseml_mlp_block``:
 ``h`` stays in LDS chunk by chunk and never reaches HBM.  The kernel holds a
 64 x D fp32 accumulator per row block in registers, so it takes D (the model
-width) of 256, 512 or 1024 only; other pairs keep their two launches.
+width) of 256, 512 or 1024 only; other pairs keep their two launches.  The
+default ``fuse_mlp_block="auto"`` binds a pair only where the single kernel
+measured faster than the two launches (:func:`mlp_block_beats_two_launches`).
 
 The launcher's calling convention is the fused launchers' (``__name__``,
 positional inputs, ``ValueError`` on arity, fresh row-major output, launch on
@@ -34,6 +36,15 @@ from .fallback import EagerFallbackGuard
 
 MLP_WIDTHS = (256, 512, 1024)
 MLP_CHUNK = 32
+# The measured crossover (``python -m fuseml_amd.calibration --mlp``, rows in
+# profiles/mlp_block_crossover.json): the single kernel streams every weight
+# through each CU once per 64-row block, so it wins only where the row blocks
+# fill the chip (at least one per CU) and the weights are small (D = 256):
+# 0.84-0.92x of the two launches' time at M >= 16384 on 256 CUs (0.98x at
+# M = 65536, I = 1024), 1.04-1.74x below that; D = 512 loses (1.06-1.41x) and
+# D = 1024 too (2.24x).
+MLP_AUTO_WIDTH = 256
+MLP_AUTO_MIN_ROW_BLOCKS = 256
 
 _DTYPES = {torch.bfloat16: _abi.BF16, torch.float16: _abi.F16}
 
@@ -51,15 +62,35 @@ def mlp_shape_supported(M: int, D: int, I: int, dtype: torch.dtype) -> Tuple[boo
     return True, "fused"
 
 
+def mlp_block_beats_two_launches(M: int, D: int, I: int) -> Tuple[bool, str]:
+    """The cost model's rule for ``fuse_mlp_block="auto"``: the single kernel
+    (with packed weights) for D = 256, I a multiple of 128 and at least
+    MLP_AUTO_MIN_ROW_BLOCKS 64-row blocks; otherwise the two launches."""
+    if D != MLP_AUTO_WIDTH:
+        return False, f"D={D}: the single kernel measured slower than two launches (D = {MLP_AUTO_WIDTH} only)"
+    if I % 128 != 0:
+        return False, f"I={I} is not a multiple of 128 (the weight-streaming kernel's slice)"
+    if -(-M // 64) < MLP_AUTO_MIN_ROW_BLOCKS:
+        return False, f"M={M}: fewer than {MLP_AUTO_MIN_ROW_BLOCKS} 64-row blocks"
+    return True, "single kernel"
+
+
 class HipMlpLauncher:
     """Callable ``(x, t(W1), b1, t(W2), b2, r) -> y`` on ``fuseml_mlp_block``."""
 
     N_INPUTS = 6
 
     def __init__(self, approximate: str = "none", eager_fn: Optional[Callable[..., Any]] = None,
-                 kernel_signature: str = "mlp_block") -> None:
+                 kernel_signature: str = "mlp_block", pack_weights: bool = True) -> None:
         self.__name__ = "fuseml_mlp_block"
         self.approximate = approximate
+        # Where the kernel streams weight fragments (D of 256 or 512, I a
+        # multiple of 128), W1 and W2 are repacked once into fragment order
+        # (fuseml_mlp_pack_weights: 4*D*I extra bytes, held here) and packed
+        # again when either weight changes (pointer, stride or in-place version).
+        self.pack_weights = pack_weights
+        self._pack: Optional[torch.Tensor] = None
+        self._pack_key: Optional[tuple] = None
         self._gelu = _abi.OP_GELU_TANH if approximate == "tanh" else _abi.OP_GELU_ERF
         self._lib = _abi.load_library()
         self._desc = _abi.MlpDesc()
@@ -116,7 +147,21 @@ class HipMlpLauncher:
         d.y, d.ldy = y.data_ptr(), D
         d.dtype = _DTYPES[dt]
         d.gelu = self._gelu
+        d.wpack = None
         stream = torch.cuda.current_stream(x.device).cuda_stream if x.device.type == "cuda" else 0
+        if self.pack_weights and isinstance(self._lib, ctypes.CDLL):
+            nbytes = self._lib.fuseml_mlp_pack_bytes(ctypes.byref(d))
+            if nbytes > 0:
+                key = (x.device, dt, D, I, w1t.data_ptr(), w1t.stride(1), w1t._version,
+                       w2t.data_ptr(), w2t.stride(1), w2t._version)
+                if key != self._pack_key:
+                    buf = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+                    rc = self._lib.fuseml_mlp_pack_weights(ctypes.byref(d), ctypes.c_void_p(buf.data_ptr()),
+                                                           ctypes.c_void_p(stream))
+                    if rc != _abi.OK:
+                        raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
+                    self._pack, self._pack_key = buf, key
+                d.wpack = self._pack.data_ptr()
         rc = self._lib.fuseml_mlp_block(ctypes.byref(d), ctypes.c_void_p(stream))
         if rc != _abi.OK:
             raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FUSEML_ABI_VERSION 4
+#define FUSEML_ABI_VERSION 5
 
 #define FUSEML_MAX_OPS 16
 #define FUSEML_MAX_OPERANDS 8
@@ -218,6 +218,10 @@ typedef struct fuseml_mlp_desc {
   int64_t ldy;
   int32_t dtype; /* FUSEML_BF16 | FUSEML_F16, for every tensor     */
   int32_t gelu;  /* FUSEML_OP_GELU_ERF | FUSEML_OP_GELU_TANH       */
+  /* Optional: W1 and W2 repacked by fuseml_mlp_pack_weights (NULL: read
+   * W1 and W2 as they are).  Used where the kernel streams weight fragments
+   * (D of 256 or 512, I a multiple of 128); w1 and w2 are still required. */
+  const void* wpack;
 } fuseml_mlp_desc;
 
 /* Launch the single-kernel MLP block on `stream`.  0 or a FUSEML_E* code. */
@@ -225,6 +229,20 @@ int fuseml_mlp_block(const fuseml_mlp_desc* desc, void* stream);
 
 /* 1 if fuseml_mlp_block accepts `desc`, 0 if not (reason in fuseml_last_error()). */
 int fuseml_mlp_block_supported(const fuseml_mlp_desc* desc);
+
+/* Bytes of the repacked weights for `desc` (4 * D * I: W1 and W2 reordered),
+ * or 0 if its shape does not stream weight fragments (D not 256 or 512, or I
+ * not a multiple of 128).  Host only. */
+int64_t fuseml_mlp_pack_bytes(const fuseml_mlp_desc* desc);
+
+/* Write desc's W1 and W2 into `wpack` (fuseml_mlp_pack_bytes(desc) bytes,
+ * 16-byte aligned) in the order the single-kernel MLP consumes them: per
+ * 128-column slice of I and per wave, each 16-byte-per-lane MFMA fragment as
+ * one contiguous 1 KB block, so every fragment load is whole cache lines
+ * (read from W1 and W2 as they are, each lane takes 32 bytes from each of 32
+ * rows).  Asynchronous on `stream`.  The caller re-packs after changing W1 or
+ * W2.  No reference counterpart: the reference has no single-kernel MLP. */
+int fuseml_mlp_pack_weights(const fuseml_mlp_desc* desc, void* wpack, void* stream);
 
 /* ------------------------------------------------------------------------
  * fp32 GEMM operands.  Writes the bf16 parts of an fp32 matrix so that the

@@ -14,7 +14,7 @@ HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))
 
 def _declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(fuseml_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*|size_t)\s+(fuseml_\w+)\s*\(", text, re.M)))
 
 
 def test_library_loads_and_abi_matches():
@@ -136,3 +136,21 @@ def test_operand_span_limit_is_per_tile():
     o.extent = 39999 * (1 << 23) + 32768
     assert lib.fuseml_gemm_epilogue_supported(ctypes.byref(d)) == 0
     assert "2 GiB" in _abi.last_error(lib)
+
+
+def test_mlp_pack_bytes_is_host_only():
+    """The repacked-weight size: 4 * D * I bytes where the single-kernel MLP
+    streams weight fragments (D of 256 or 512, I a multiple of 128), else 0."""
+    lib = _abi.load_library()
+    d = _abi.MlpDesc()
+    d.M, d.D, d.I = 1000, 256, 1024
+    d.x, d.ldx, d.w1, d.ldw1, d.b1 = 0x10000, 256, 0x20000, 256, 0x30000
+    d.w2, d.ldw2, d.y, d.ldy = 0x40000, 1024, 0x50000, 256
+    d.dtype, d.gelu = _abi.BF16, _abi.OP_GELU_ERF
+    assert lib.fuseml_mlp_pack_bytes(ctypes.byref(d)) == 4 * 256 * 1024
+    d.I, d.ldw2 = 96, 96                      # not a multiple of 128: the D-split kernel, no packing
+    assert lib.fuseml_mlp_pack_bytes(ctypes.byref(d)) == 0
+    d.D, d.I, d.ldx, d.ldw1, d.ldw2, d.ldy = 1024, 1024, 1024, 1024, 1024, 1024
+    assert lib.fuseml_mlp_pack_bytes(ctypes.byref(d)) == 0
+    d.D = 300                                 # unsupported width: invalid descriptor
+    assert lib.fuseml_mlp_pack_bytes(ctypes.byref(d)) == 0

@@ -2,7 +2,10 @@
 
 ``profiles/cost_model_calibration.json`` is the output of
 ``python -m fuseml_amd.calibration`` on one MI355X: per GEMM group, the fused
-kernel, the eager ops and hipBLASLt's plain GEMM on the same inputs.  For every
+kernel, the eager ops and hipBLASLt's plain GEMM on the same inputs.
+``profiles/mlp_block_crossover.json`` (``--mlp``) times compiled MLP blocks with
+two launches and with the single-kernel MLP; the default
+``fuse_mlp_block="auto"`` rule must pick the faster one.  For every
 row whose fused and eager times differ by more than the tie margin, the rules
 the compiler applies today (:func:`fused_beats_eager` and the few-tile rule of
 :func:`trigger_is_fusible`) must pick the measured winner; a row within the
@@ -18,9 +21,11 @@ import torch
 
 from fuseml_amd import calibration as cal
 from fuseml_amd.compiler import LONG_K, MIN_TILES_LONG_K, epilogue_passes, fused_beats_eager
+from fuseml_amd.mlp import mlp_block_beats_two_launches
 
-PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "profiles",
-                    "cost_model_calibration.json")
+PROFILES = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "profiles")
+PATH = os.path.join(PROFILES, "cost_model_calibration.json")
+MLP_PATH = os.path.join(PROFILES, "mlp_block_crossover.json")
 # |fused / eager - 1| below this is a tie: the same rows measured on two boxes
 # of the pool differ by 1-2%, and near the crossover the linear rule may give
 # up a few per cent (bias + residual at K = 2048: fused 3.4% faster, sent to
@@ -60,3 +65,23 @@ def test_rule_picks_the_measured_winner(row):
         pytest.skip(f"tie: fused/eager = {ratio:.3f}")
     assert _decision(row) == (ratio < 1.0), (
         f"{row['group']}: fused {row['fused_ms']} ms, eager {row['eager_ms']} ms, rule fuses={_decision(row)}")
+
+
+def _mlp_rows():
+    with open(MLP_PATH) as f:
+        return json.load(f)["rows"]
+
+
+def test_mlp_crossover_covers_both_outcomes():
+    rows = _mlp_rows()
+    assert any(r["single_over_two"] < 1 - TIE for r in rows) and any(r["single_over_two"] > 1 + TIE for r in rows)
+    assert {256, 512, 1024} <= {r["D"] for r in rows}
+
+
+@pytest.mark.parametrize("row", _mlp_rows(), ids=lambda r: f"M{r['M']}-D{r['D']}-I{r['I']}")
+def test_mlp_rule_picks_the_measured_winner(row):
+    ratio = row["single_over_two"]
+    if abs(ratio - 1.0) < TIE:
+        pytest.skip(f"tie: single/two = {ratio:.3f}")
+    binds = mlp_block_beats_two_launches(row["M"], row["D"], row["I"])[0]
+    assert binds == (ratio < 1.0), f"{row}: rule binds={binds}"

@@ -1,9 +1,11 @@
 """The single-kernel MLP block's host side on the CPU (no kernel launch).
 
 * ``FuseMLCompiler(fuse_mlp_block=True)`` binds the two groups of
-  ``linear2(gelu(linear1(x))) + x`` to one ``HipMlpLauncher`` (default: the
-  reference's two groups); the launch is forced onto its eager fallback, which
-  chains the two groups' original nodes, so the compiled module equals eager.
+  ``linear2(gelu(linear1(x))) + x`` to one ``HipMlpLauncher``; the default
+  (``"auto"``) binds them only where the measured rule says the single kernel
+  is faster, else keeps the reference's two groups.  The launch is forced onto
+  its eager fallback, which chains the two groups' original nodes, so the
+  compiled module equals eager.
 * The launcher fills ``fuseml_mlp_desc`` from the graph's layouts.
 * The shape rule mirrors the kernel's limits.
 """
@@ -17,7 +19,7 @@ import fuseml_amd.compiler as comp
 from fuseml_amd import _abi
 from fuseml_amd.compiler import FuseMLCompiler
 from fuseml_amd.fallback import FORCE_FAIL_ENV
-from fuseml_amd.mlp import HipMlpLauncher, mlp_shape_supported
+from fuseml_amd.mlp import HipMlpLauncher, mlp_block_beats_two_launches, mlp_shape_supported
 from fuseml_amd.workloads import StackedMLP, TransformerMLP
 
 BF = torch.bfloat16
@@ -43,7 +45,7 @@ def test_mlp_block_opt_in_binds_one_launcher(monkeypatch, approximate):
     assert be.launchers[0].approximate == approximate and be.launchers[0].fallback_count == 1
 
 
-def test_mlp_block_off_by_default_keeps_two_groups(monkeypatch):
+def test_mlp_block_small_batch_keeps_two_groups_by_default(monkeypatch):
     torch.manual_seed(0)
     m = TransformerMLP(256, 1024).to(BF).eval()
     x = torch.randn(64, 256, dtype=BF)
@@ -53,6 +55,39 @@ def test_mlp_block_off_by_default_keeps_two_groups(monkeypatch):
         out = _compile(m, be)(x)
     assert torch.equal(out, m(x))
     assert len(be.launchers) == 2 and not any(isinstance(l, HipMlpLauncher) for l in be.launchers)
+
+
+def test_auto_rule_follows_the_measured_crossover():
+    assert mlp_block_beats_two_launches(16384, 256, 1024)[0]          # memory_bound preset
+    assert mlp_block_beats_two_launches(65536, 256, 4096)[0]
+    assert not mlp_block_beats_two_launches(8192, 256, 1024)[0]       # fewer 64-row blocks than CUs
+    assert not mlp_block_beats_two_launches(16384, 512, 2048)[0]      # D = 512 ties at best
+    assert not mlp_block_beats_two_launches(16384, 1024, 4096)[0]     # C2: D = 1024
+    assert not mlp_block_beats_two_launches(16384, 256, 96)[0]        # I not a multiple of 128
+
+
+def test_auto_binds_where_the_single_kernel_wins(monkeypatch):
+    """Default options: the memory_bound shape (x[16384,256] -> 1024 -> 256)
+    runs as one single-kernel MLP launch; a D = 512 block keeps two launches."""
+    torch.manual_seed(0)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    m = TransformerMLP(256, 1024).to(BF).eval()
+    x = torch.randn(16384, 256, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False)
+    with torch.no_grad():
+        assert torch.equal(_compile(m, be)(x), m(x))
+    assert len(be.launchers) == 1 and isinstance(be.launchers[0], HipMlpLauncher)
+    m = TransformerMLP(512, 1024).to(BF).eval()
+    x = torch.randn(16384, 512, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False)
+    with torch.no_grad():
+        assert torch.equal(_compile(m, be)(x), m(x))
+    assert len(be.launchers) == 2 and not any(isinstance(l, HipMlpLauncher) for l in be.launchers)
+
+
+def test_fuse_mlp_block_rejects_unknown_modes():
+    with pytest.raises(ValueError):
+        FuseMLCompiler(fuse_mlp_block="always")
 
 
 def test_mlp_block_stacked_blocks_each_one_launcher(monkeypatch):
