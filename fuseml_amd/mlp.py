@@ -75,6 +75,24 @@ def mlp_block_beats_two_launches(M: int, D: int, I: int) -> Tuple[bool, str]:
     return True, "single kernel"
 
 
+_WORD = 8
+_MW = {f: getattr(_abi.MlpDesc, f).offset // _WORD for f in ("x", "w1", "b1", "w2", "b2", "r", "y", "wpack")}
+
+
+class _MlpPlan:
+    """What a call needs that depends only on its input signature: the
+    descriptor with every non-pointer field filled (written through ``words``,
+    the descriptor as uint64 words) and the packed-weight size (0: none)."""
+
+    __slots__ = ("desc", "words", "desc_ref", "M", "D", "dtype", "pack_bytes")
+
+    def __init__(self, desc: "_abi.MlpDesc", M: int, D: int, dtype: torch.dtype, pack_bytes: int) -> None:
+        self.desc = desc
+        self.words = (ctypes.c_uint64 * (ctypes.sizeof(_abi.MlpDesc) // _WORD)).from_buffer(desc)
+        self.desc_ref = ctypes.byref(desc)
+        self.M, self.D, self.dtype, self.pack_bytes = M, D, dtype, pack_bytes
+
+
 class HipMlpLauncher:
     """Callable ``(x, t(W1), b1, t(W2), b2, r) -> y`` on ``fuseml_mlp_block``."""
 
@@ -91,6 +109,9 @@ class HipMlpLauncher:
         self.pack_weights = pack_weights
         self._pack: Optional[torch.Tensor] = None
         self._pack_key: Optional[tuple] = None
+        # Per input signature (shapes, strides, dtypes, device): a plan whose
+        # calls only write pointers (see launch).
+        self._plans: Dict[tuple, _MlpPlan] = {}
         self._gelu = _abi.OP_GELU_TANH if approximate == "tanh" else _abi.OP_GELU_ERF
         self._lib = _abi.load_library()
         self._desc = _abi.MlpDesc()
@@ -106,6 +127,64 @@ class HipMlpLauncher:
 
     def launch(self, x: torch.Tensor, w1t: torch.Tensor, b1: torch.Tensor, w2t: torch.Tensor,
                b2: Optional[torch.Tensor], r: Optional[torch.Tensor]) -> torch.Tensor:
+        """A call whose signature was seen before writes only the pointers into
+        that signature's descriptor; the first call of a signature checks and
+        fills it (and calls with layouts that need copies always take that path)."""
+        if isinstance(self._lib, ctypes.CDLL):
+            key = (x.shape, x.stride(), x.dtype, x.device, w1t.shape, w1t.stride(), w1t.dtype, w1t.get_device(),
+                   b1.shape, b1.stride(), b1.dtype, b1.get_device(), w2t.stride(), w2t.dtype, w2t.get_device(),
+                   None if b2 is None else (b2.shape, b2.stride(), b2.dtype, b2.get_device()),
+                   None if r is None else (r.shape, r.stride(), r.dtype, r.get_device()))
+            plan = self._plans.get(key)
+            if plan is not None:
+                return self._launch_planned(plan, key, x, w1t, b1, w2t, b2, r)
+            y = self._launch_checked(x, w1t, b1, w2t, b2, r)
+            if self._plan_ok:
+                d = _abi.MlpDesc()
+                ctypes.memmove(ctypes.byref(d), ctypes.byref(self._desc), ctypes.sizeof(d))
+                self._plans[key] = _MlpPlan(d, int(x.shape[0]), int(x.shape[1]), x.dtype, self._plan_pack_bytes)
+            return y
+        return self._launch_checked(x, w1t, b1, w2t, b2, r)
+
+    def _launch_planned(self, plan: "_MlpPlan", key: tuple, x: torch.Tensor, w1t: torch.Tensor,
+                        b1: torch.Tensor, w2t: torch.Tensor, b2: Optional[torch.Tensor],
+                        r: Optional[torch.Tensor]) -> torch.Tensor:
+        w = plan.words
+        w[_MW["x"]] = x.data_ptr()
+        w[_MW["w1"]] = w1t.data_ptr()
+        w[_MW["b1"]] = b1.data_ptr()
+        w[_MW["w2"]] = w2t.data_ptr()
+        w[_MW["b2"]] = 0 if b2 is None else b2.data_ptr()
+        w[_MW["r"]] = 0 if r is None else r.data_ptr()
+        y = torch.empty((plan.M, plan.D), dtype=plan.dtype, device=x.device)
+        w[_MW["y"]] = y.data_ptr()
+        stream = torch._C._cuda_getCurrentRawStream(x.get_device())
+        w[_MW["wpack"]] = self._packed(plan.desc_ref, plan.pack_bytes, x, w1t, w2t, stream) if plan.pack_bytes else 0
+        rc = self._lib.fuseml_mlp_block(plan.desc_ref, ctypes.c_void_p(stream))
+        if rc != _abi.OK:
+            raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
+        self.launch_count += 1
+        return y
+
+    def _packed(self, desc_ref: Any, nbytes: int, x: torch.Tensor, w1t: torch.Tensor, w2t: torch.Tensor,
+                stream: int) -> int:
+        """The packed weights' address (packed again when W1 or W2 changed)."""
+        key = (x.device, nbytes, w1t.data_ptr(), w1t.stride(1), w1t._version, w2t.data_ptr(), w2t.stride(1),
+               w2t._version)
+        if key != self._pack_key:
+            buf = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+            rc = self._lib.fuseml_mlp_pack_weights(desc_ref, ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(stream))
+            if rc != _abi.OK:
+                raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
+            self._pack, self._pack_key = buf, key
+        return self._pack.data_ptr()
+
+    def _launch_checked(self, x: torch.Tensor, w1t: torch.Tensor, b1: torch.Tensor, w2t: torch.Tensor,
+                        b2: Optional[torch.Tensor], r: Optional[torch.Tensor]) -> torch.Tensor:
+        # whether this call's descriptor may serve later calls of its signature
+        # (operands used in place, not copied), and its packed-weight size
+        self._plan_ok = False
+        self._plan_pack_bytes = 0
         if x.dim() != 2 or w1t.dim() != 2 or w2t.dim() != 2:
             raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "mlp_block takes 2-D x and weights")
         M, D = x.shape
@@ -122,6 +201,8 @@ class HipMlpLauncher:
                 (b2 is not None and b2.shape != (D,)) or (r is not None and tuple(r.shape) != (M, D)):
             raise _abi.FuseMLHipError(_abi.EUNSUPPORTED, "mlp_block: operand shapes do not chain")
         # K-contiguous operands (the graph's layouts: x row-major, t(W) views).
+        in_place = (x.stride(1) == 1 and w1t.stride(0) == 1 and w2t.stride(0) == 1 and b1.is_contiguous()
+                    and (b2 is None or b2.is_contiguous()) and (r is None or r.stride(1) == 1))
         if x.stride(1) != 1:
             x = x.contiguous()
         if w1t.stride(0) != 1:
@@ -149,23 +230,16 @@ class HipMlpLauncher:
         d.gelu = self._gelu
         d.wpack = None
         stream = torch.cuda.current_stream(x.device).cuda_stream if x.device.type == "cuda" else 0
+        nbytes = 0
         if self.pack_weights and isinstance(self._lib, ctypes.CDLL):
             nbytes = self._lib.fuseml_mlp_pack_bytes(ctypes.byref(d))
             if nbytes > 0:
-                key = (x.device, dt, D, I, w1t.data_ptr(), w1t.stride(1), w1t._version,
-                       w2t.data_ptr(), w2t.stride(1), w2t._version)
-                if key != self._pack_key:
-                    buf = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
-                    rc = self._lib.fuseml_mlp_pack_weights(ctypes.byref(d), ctypes.c_void_p(buf.data_ptr()),
-                                                           ctypes.c_void_p(stream))
-                    if rc != _abi.OK:
-                        raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
-                    self._pack, self._pack_key = buf, key
-                d.wpack = self._pack.data_ptr()
+                d.wpack = self._packed(ctypes.byref(d), nbytes, x, w1t, w2t, stream)
         rc = self._lib.fuseml_mlp_block(ctypes.byref(d), ctypes.c_void_p(stream))
         if rc != _abi.OK:
             raise _abi.FuseMLHipError(rc, _abi.last_error(self._lib))
         self.launch_count += 1
+        self._plan_ok, self._plan_pack_bytes = in_place, nbytes
         return y
 
     def __call__(self, *inputs: Any) -> torch.Tensor:
