@@ -659,24 +659,28 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       const int k0 = kt * BK;
       const uint32_t kb = (uint32_t)(k0 * 2);
       char* st = smem + slot * STAGE;
+      // The whole-stage schedule runs only for K % 64 == 0 (choose_config): a
+      // stage is wholly inside or outside [0, K), so its k offset is one
+      // uniform value, passed as the buffer instruction's scalar offset (no
+      // per-lane arithmetic: 33 fewer VALU instructions per stage, ~1% on the
+      // bench shapes).  A stage past K re-reads stage 0's k range (in bounds);
+      // nothing consumes it.
+      const uint32_t sk = (SCHED == 6 && kt < nk) ? kb : 0u;
       static_for<decltype(c0)::value, decltype(c1)::value>([&](auto c) {
         uint32_t off;
         __amdgpu_buffer_rsrc_t r;
         if constexpr (c < A_DMA) {
-          // The whole-stage schedule runs only for K % 64 == 0 (choose_config):
-          // a stage is wholly inside or outside [0, K), and the per-chunk k
-          // offsets need no registers across its K loop.
-          if constexpr (SCHED == 6) off = kt < nk ? a_off[c] + kb : kOOB;
+          if constexpr (SCHED == 6) off = a_off[c];
           else off = (k0 + a_k[c] < K) ? a_off[c] + kb : kOOB;
           r = ra;
         } else {
           constexpr int i = c - A_DMA;
-          if constexpr (SCHED == 6) off = kt < nk ? b_off[i] + kb : kOOB;
+          if constexpr (SCHED == 6) off = b_off[i];
           else off = (k0 + b_k[i] < K) ? b_off[i] + kb : kOOB;
           r = rb;
         }
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            r, (__attribute__((address_space(3))) void*)(st + (wave + NW * c) * 1024), 16, off, 0, 0, 0);
+            r, (__attribute__((address_space(3))) void*)(st + (wave + NW * c) * 1024), 16, off, sk, 0, 0);
       });
     };
     auto load_stage = [&](int kt, int slot) {
@@ -1537,12 +1541,22 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
 #pragma clang loop unroll(disable)
       for (int i = 0; i < NI; ++i) {
         f32x16_t A[NJ];
-        static_for<0, NI>([&](auto ii) {
-          if (i == ii) {
-            static_for<0, NJ>([&](auto j) { A[j] = acc[ii][j]; });
-            asm volatile("; column block %0" ::"n"((int)ii));
-          }
-        });
+        // An if/else chain, so that every path defines A: with four
+        // independent ifs the compiler carries an undefined path's registers
+        // around the loop (32 64-bit copies per column block).
+        static_assert(NI == 4, "four column blocks");
+        auto pick = [&](auto ii) {
+          static_for<0, NJ>([&](auto j) { A[j] = acc[ii][j]; });
+          asm volatile("; column block %0" ::"n"((int)ii));
+        };
+        if (i == 0)
+          pick(std::integral_constant<int, 0>{});
+        else if (i == 1)
+          pick(std::integral_constant<int, 1>{});
+        else if (i == 2)
+          pick(std::integral_constant<int, 2>{});
+        else
+          pick(std::integral_constant<int, 3>{});
         static_for<0, NJ>([&](auto j) {
           static_for<0, 16>([&](auto r) {
             float x = A[j][(int)r];
