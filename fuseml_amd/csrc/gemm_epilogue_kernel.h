@@ -755,10 +755,13 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       //   k-step 0: MFMAs while the fragments of k-steps 1-3 are read;
       //   barrier 1 (after this wave's reads): no wave reads slot k % 2 any more;
       //   k-steps 1-3: MFMAs while stage k+2's DMA goes into slot k % 2, spread
-      //   over the three k-steps (barrier 2 before k-step 3: stage k+1 landed
-      //   and visible); k-step 3 also reads stage k+1's k-step 0 fragments.
+      //   over the three k-steps (barrier 2 in k-step 3: stage k+1 landed and
+      //   visible); k-step 3 also reads stage k+1's k-step 0 fragments.
       // Each k-step then carries at most ~21 KB of DMA writes or 24 KB of reads
-      // per wave-quad, instead of two k-steps carrying both.
+      // per wave-quad, instead of two k-steps carrying both.  Each barrier sits
+      // two MFMAs into its k-step (those two need nothing it guards), so the
+      // reads that barrier 1 waits for have two more MFMAs to land (C5 -0.6
+      // and -1.3%).
       static_assert(S == 2 && KS == 4 && NI == 4 && NJ == 4 && LPS == 16, "one-wave whole-stage geometry");
       i32x4_t fr[KS][NI + NJ];
       auto rd = [&](const char* st, auto ks, auto f) {
@@ -780,26 +783,36 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
       // k-step ks: MFMAs from fr[ks]; fragment reads [r0, r1) of stage `rst`
       // (read r: k-step r / 8, fragment r % 8) and DMA chunks [c0, c1) of stage
       // kt, each spread evenly over the 16 MFMAs.
-      auto kstep = [&](auto ks, const char* rst, auto r0, auto r1, int kt, int slot, auto c0, auto c1, auto tail) {
+      // MFMAs [q0, q1) of k-step ks, the reads and DMAs spread over them.
+      auto kstep_q = [&](auto ks, const char* rst, auto r0, auto r1, int kt, int slot, auto c0, auto c1, auto tail,
+                         auto q0, auto q1) {
         constexpr int n_rd = decltype(r1)::value - decltype(r0)::value;
         constexpr int n_dma = decltype(c1)::value - decltype(c0)::value;
-        static_for<0, NI * NJ>([&](auto q) {
+        constexpr int Q0 = decltype(q0)::value, NQ = decltype(q1)::value - Q0;
+        static_for<0, NQ>([&](auto qq) {
+          constexpr int q = Q0 + qq;
           constexpr int i = q / NJ, j = q % NJ;
           acc[i][j] = mfma32<T>(fr[ks][i], fr[ks][NI + j], acc[i][j]);
           static_for<0, n_rd>([&](auto m) {
-            if constexpr ((m * (NI * NJ)) / n_rd == q) {
+            if constexpr ((m * NQ) / n_rd == qq) {
               constexpr int r = decltype(r0)::value + m;
               rd(rst, std::integral_constant<int, r / 8>{}, std::integral_constant<int, r % 8>{});
             }
           });
           static_for<0, n_dma>([&](auto m) {
-            if constexpr ((m * (NI * NJ)) / n_dma == q) {
+            if constexpr ((m * NQ) / n_dma == qq) {
               constexpr int c = decltype(c0)::value + m;
               issue(kt, slot, std::integral_constant<int, c>{}, std::integral_constant<int, c + 1>{}, tail);
             }
           });
           __builtin_amdgcn_sched_barrier(0);
         });
+      };
+      using QA = std::integral_constant<int, 0>;
+      using QS = std::integral_constant<int, 2>;
+      using QE = std::integral_constant<int, NI * NJ>;
+      auto kstep = [&](auto ks, const char* rst, auto r0, auto r1, int kt, int slot, auto c0, auto c1, auto tail) {
+        kstep_q(ks, rst, r0, r1, kt, slot, c0, c1, tail, QA{}, QE{});
       };
       using I0 = std::integral_constant<int, 0>;
       using I1 = std::integral_constant<int, 1>;
@@ -815,13 +828,15 @@ void gemm_epilogue_kernel(const fuseml_gemm_desc d_arg) {
         const char* st = smem + (k & 1) * STAGE;
         const char* nst = smem + ((k + 1) & 1) * STAGE;
         kstep(I0{}, st, R8{}, R32{}, k + 2, k & 1, R0{}, R0{}, tail);
+        kstep_q(I1{}, st, R0{}, R0{}, k + 2, k & 1, R0{}, R0{}, tail, QA{}, QS{});
         wait_lgkmcnt0();
         barrier();  // slot k % 2 retired
-        kstep(I1{}, st, R0{}, R0{}, k + 2, k & 1, R0{}, D6{}, tail);
+        kstep_q(I1{}, st, R0{}, R0{}, k + 2, k & 1, R0{}, D6{}, tail, QS{}, QE{});
         kstep(I2{}, st, R0{}, R0{}, k + 2, k & 1, D6{}, D11{}, tail);
+        kstep_q(I3{}, nst, R0{}, R0{}, k + 2, k & 1, D11{}, D11{}, tail, QA{}, QS{});
         wait_vmcnt<11>();  // stage k+1 (only stage k+2's first 11 chunks are younger)
         barrier();
-        kstep(I3{}, nst, R0{}, R8{}, k + 2, k & 1, D11{}, D16{}, tail);
+        kstep_q(I3{}, nst, R0{}, R8{}, k + 2, k & 1, D11{}, D16{}, tail, QS{}, QE{});
       };
       using Tail = std::true_type;
       issue(0, 0, R0{}, D16{}, Tail{});
