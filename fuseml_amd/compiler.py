@@ -63,12 +63,12 @@ logger = logging.getLogger("fuseml_amd")
 REFERENCE_MIN_OUTPUT_ELEMENTS = 500_000
 MIN_FUSION_OUTPUT_ELEMENTS = 0
 LONG_K = 2048
-MIN_TILES_LONG_K = 256  # 128x128 output tiles; MI355X has 256 CUs
+MIN_TILES_LONG_K = 512  # 128x128 output tiles: two per CU of MI355X's 256
 # Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the
 # eager path would run over the [M,N] output) - K_CROSSOVER_OFFSET: the
 # crossover measured on MI355X (fuseml_amd/calibration.py; the measurement is
-# profiles/cost_model_calibration.json): 1536 for one pass, 9216 for four.
-K_PER_EPILOGUE_PASS = 2560
+# profiles/cost_model_calibration.json): 2048 for one pass, 11264 for four.
+K_PER_EPILOGUE_PASS = 3072
 K_CROSSOVER_OFFSET = 1024
 # fp32 operands run as a three-term bf16 split product (K' = 3 ceil8(K)).
 SUPPORTED_GEMM_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
@@ -185,7 +185,7 @@ def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSIO
     k_loop = effective_k(K, m1.dtype)
     if k_loop >= LONG_K and tiles < min_tiles_long_k:
         k_txt = f"K={K}" if k_loop == K else f"K={K} (a K loop of {k_loop})"
-        return False, f"{tiles} output tiles at {k_txt}: fewer tiles than CUs with a long K loop"
+        return False, f"{tiles} output tiles at {k_txt}: fewer than two tiles per CU with a long K loop"
     return True, "fused"
 
 
@@ -276,12 +276,13 @@ def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOG
     pass at 16384x4096, the same at every K), while the fused kernel pays its
     epilogue (which grows slower than the number of ops) plus a K loop that
     falls behind hipBLASLt's as K grows.  So the crossover K grows with the
-    passes: one pass fuses at K = 1024 (bias + GELU 16384x4096: 0.157 against
-    eager 0.168 ms), ties at K = 2048 and loses from K = 4096 (8192x16384: 0.852
-    against 0.836 ms; bias + residual at K = 16384: 0.776 against 0.723 ms);
-    four passes still win at K = 8192 (0.80 against 0.90 ms).  Rule: fuse iff
-    K <= k_per_pass * passes - k_offset (2560 and 1024: K <= 1536 for one pass,
-    4096 for two, 9216 for four); k_per_pass = 0 always fuses.
+    passes: one pass fuses at K = 1024 (bias + GELU 16384x4096: 0.161 against
+    eager 0.172 ms) and K = 2048 (bias + residual 0.066 against 0.069 ms), ties
+    at K = 4096 (8192x16384 bias + GELU: 0.854 against 0.851 ms) and loses
+    beyond (bias + residual at K = 16384: 0.793 against 0.737 ms); four passes
+    still win at K = 8192 (0.80 against 0.89 ms).  Rule: fuse iff
+    K <= k_per_pass * passes - k_offset (3072 and 1024: K <= 2048 for one pass,
+    5120 for two, 11264 for four); k_per_pass = 0 always fuses.
 
     fp32 groups always fuse: eager runs an fp32 GEMM at the fp32 MFMA rate
     (157 TFLOP/s peak), the split product at a third of the bf16 rate."""

@@ -189,8 +189,8 @@ def test_cost_model_rules():
 
 
 def test_cost_model_few_tiles_long_k():
-    """K >= 2048 with fewer 128x128 output tiles than CUs stays eager; a full
-    round of tiles, or a short K loop, is fused."""
+    """K >= 2048 with fewer 128x128 output tiles than two per CU stays eager;
+    two full rounds of tiles, or a short K loop, is fused."""
     from torch.fx.experimental.proxy_tensor import make_fx
 
     def f(x, w):
@@ -203,7 +203,8 @@ def test_cost_model_few_tiles_long_k():
     ok, why = trigger_is_fusible(node(1024, 2048, 1024))      # 8 x 8 = 64 tiles
     assert ok is False and "64 output tiles at K=2048" in why
     assert trigger_is_fusible(node(1024, 2048, 1024), min_tiles_long_k=0)[0]
-    assert trigger_is_fusible(node(2048, 2048, 2048))[0]       # 16 x 16 = 256 tiles
+    assert not trigger_is_fusible(node(2048, 2048, 2048))[0]   # 16 x 16 = 256 tiles
+    assert trigger_is_fusible(node(4096, 2048, 2048))[0]       # 32 x 16 = 512 tiles
     assert trigger_is_fusible(node(1024, 2040, 1024))[0]       # K < 2048
     assert trigger_is_fusible(node(1024, 1024, 1024))[0]
 
@@ -263,8 +264,8 @@ def test_epilogue_passes_and_crossover_rule():
     assert epilogue_passes(mm_add, gemm_is_addmm=True) == 0
     assert epilogue_passes(mm_add_gelu, gemm_is_addmm=False) == 2
     assert fused_beats_eager(mm_add, 1024, gemm_is_addmm=False)[0]
-    assert fused_beats_eager(mm_add_gelu, 2048, gemm_is_addmm=False)[0]
-    assert not fused_beats_eager(mm_add_gelu, 2048, gemm_is_addmm=True)[0]
+    assert fused_beats_eager(mm_add_gelu, 4096, gemm_is_addmm=False)[0]
+    assert not fused_beats_eager(mm_add_gelu, 4096, gemm_is_addmm=True)[0]
 
 
 class _MmAddGelu(nn.Module):
