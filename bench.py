@@ -399,7 +399,8 @@ def preset_traffic(kind: str, M: int, D: int, I: int, blocks: int) -> dict:
     * eager: addmm (x, W1, b1 -> t), GELU (t -> t), for the activation-heavy
       block * 0.5 and + 0.125 (t -> t each), addmm (t, W2, b2 -> u), + x (u, x -> y);
     * fused (two launches per block): (x, W1, b1 -> h), (h, W2, b2, x -> y);
-    * single-kernel MLP: (x, W1, b1, W2, b2 -> y), x read once as input and residual;
+    * single-kernel MLP: (x, W1, b1, W2, b2 -> y), x read once as input and residual
+      (the activation-heavy block's scale and shift run inside it);
     * compulsory: the forward's input, every weight and bias, its output.
 
     "eliminated" is 1 - (path - compulsory) / (eager - compulsory): the share
@@ -416,8 +417,7 @@ def preset_traffic(kind: str, M: int, D: int, I: int, blocks: int) -> dict:
     out = {"eager_bytes": eager, "fused_bytes": fused, "compulsory_bytes": comp,
            "fused_eliminated": round(1 - (fused - comp) / (eager - comp), 4),
            "fused_total_saved": round(1 - fused / eager, 4)}
-    if kind != "activation_heavy":
-        out.update(single_kernel_bytes=single, single_kernel_eliminated=round(1 - (single - comp) / (eager - comp), 4))
+    out.update(single_kernel_bytes=single, single_kernel_eliminated=round(1 - (single - comp) / (eager - comp), 4))
     return out
 
 
@@ -473,9 +473,8 @@ def _presets(args, dev):
             # all_fused: every group as its own launch (no single-kernel MLP)
             paths = {"compiled": {}, "all_fused": dict(k_per_epilogue_pass=0, min_tiles_long_k=0,
                                                        min_output_elements=0, fuse_mlp_block=False)}
-            if kind != "activation_heavy":
-                paths["single_kernel_mlp"] = dict(fuse_mlp_block=True, k_per_epilogue_pass=0, min_tiles_long_k=0,
-                                                  min_output_elements=0)
+            paths["single_kernel_mlp"] = dict(fuse_mlp_block=True, k_per_epilogue_pass=0, min_tiles_long_k=0,
+                                              min_output_elements=0)
             for label, kw in paths.items():
                 torch._dynamo.reset()
                 be = FuseMLCompiler(**kw)

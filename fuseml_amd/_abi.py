@@ -17,10 +17,11 @@ import os
 import threading
 from typing import Optional
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 MAX_OPS = 16
 MAX_OPERANDS = 8
 MAX_EXTRA_OUT = 4
+MLP_MAX_POST = 4
 
 # Element types.
 BF16, F16, F32 = 0, 1, 2
@@ -142,7 +143,7 @@ class GemmDesc(ctypes.Structure):
 
 
 class MlpDesc(ctypes.Structure):
-    """fuseml_mlp_desc: the single-kernel MLP block (y = GELU(x W1^T + b1) W2^T + b2 + r)."""
+    """fuseml_mlp_desc: the single-kernel MLP block (y = post(GELU(x W1^T + b1)) W2^T + b2 + r)."""
 
     _fields_ = [
         ("M", ctypes.c_int64),
@@ -163,6 +164,9 @@ class MlpDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("gelu", ctypes.c_int32),
         ("wpack", ctypes.c_void_p),
+        ("n_post", ctypes.c_int32),
+        ("post_kind", ctypes.c_int32 * MLP_MAX_POST),
+        ("post_scalar", ctypes.c_float * MLP_MAX_POST),
     ]
 
 

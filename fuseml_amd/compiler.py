@@ -491,7 +491,7 @@ class FuseMLCompiler:
 
     def _bind_mlp_blocks(self, gm: torch.fx.GraphModule, placeholders: List[torch.fx.Node],
                          strategies: set) -> List[torch.fx.Node]:
-        """Bind each (GEMM1+bias+GELU, GEMM2+bias+residual) placeholder pair whose
+        """Bind each (GEMM1+bias+GELU[+scalar ops], GEMM2+bias+residual) placeholder pair whose
         GELU output feeds only the second GEMM to one single-kernel MLP launcher
         (``fuse_mlp_block=True``, or ``"auto"`` where the single kernel measured
         faster); return the placeholders left to bind."""
@@ -543,7 +543,7 @@ class FuseMLCompiler:
                 continue
             eager = mlp_eager_fn(EagerGroupLauncher(g1.eager_module), EagerGroupLauncher(g2.eager_module),
                                  n1, n2, slots1, slots2)
-            launcher = HipMlpLauncher(m1["approximate"], eager_fn=eager,
+            launcher = HipMlpLauncher(m1["approximate"], eager_fn=eager, post=m1["post"],
                                       kernel_signature=f"{g1!r} + {g2!r}: mlp_block")
             args = (ph1.args[m1["x"]], ph1.args[m1["w1t"]], ph1.args[m1["b1"]],
                     ph2.args[m2["w2t"]], ph2.args[m2["b2"]], ph2.args[m2["r"]])

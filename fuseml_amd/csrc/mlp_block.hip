@@ -1,14 +1,16 @@
 // mlp_block.hip — the whole MLP block in one kernel: the intermediate
 // activation h never leaves the CU.
 //
-//   h = GELU(x @ W1^T + b1)            x [M, D], W1 [I, D], b1 [I]
+//   h = post(GELU(x @ W1^T + b1))      x [M, D], W1 [I, D], b1 [I]
 //   y = h @ W2^T + b2 + r               W2 [D, I], b2 [D], r [M, D] (residual)
 //
 // The reference cannot form this group: an addmm ends a group (BARRIER_OPS,
 // fuseml/passes/topology.py:63-64) and absorption needs a single user
 // (fuseml/passes/fusion_pass.py:203-206), so the block is two launches of its
 // generated kernel with h written to and read back from HBM (the two-group
-// module of benchmarks/bench_mlp_block.py:160-182).
+// module of benchmarks/bench_mlp_block.py:160-182).  post is the descriptor's
+// scalar ops (scale, add) on GELU's output: the activation-heavy block's
+// "* 0.5 + 0.125" (bench_mlp_block.py:185-207).
 //
 // Structure (one workgroup of 4 waves per CU, persistent over 64-row blocks):
 //   * The row block's y accumulator, 64 x D fp32, stays in AGPRs for the whole
@@ -173,6 +175,23 @@ __device__ __forceinline__ void static_for(F&& f) {
     f(std::integral_constant<int, B>{});
     static_for<B + 1, E>(f);
   }
+}
+
+// The descriptor's post-GELU scalar ops on N values, in order, in fp32: each op
+// over all N values under one uniform branch (constant indices into the
+// descriptor, so its arrays stay in scalar registers).
+template <int N>
+__device__ __forceinline__ void post_ops(const fuseml_mlp_desc& d, float* v) {
+  static_for<0, FUSEML_MLP_MAX_POST>([&](auto p) {
+    if (p < d.n_post) {
+      const float sc = d.post_scalar[p];
+      if (d.post_kind[p] == FUSEML_OP_SCALE) {
+        static_for<0, N>([&](auto e) { v[e] = v[e] * sc; });
+      } else {
+        static_for<0, N>([&](auto e) { v[e] = v[e] + sc; });
+      }
+    }
+  });
 }
 
 // Epilogue of a row block: y = acc + b2 + r as 16-bit.  acc[mb][db][r] is
@@ -352,6 +371,7 @@ void mlp_block_kernel(const fuseml_mlp_desc d) {
           else
             v[e] = gelu_erf(v[e]);
         });
+        post_ops<8>(d, v);
         const i32x4_t hv = {(int)pack2<T>(v[0], v[1]), (int)pack2<T>(v[2], v[3]), (int)pack2<T>(v[4], v[5]),
                             (int)pack2<T>(v[6], v[7])};
         *reinterpret_cast<i32x4_t*>(part + part_chunk(m, 2 * j)) = hv;
@@ -509,21 +529,28 @@ void mlp_block_kernel_isplit(const fuseml_mlp_desc d) {
           h1[mb] = mfma32<T>(w, xf, h1[mb]);
         });
       });
-      // h1[mb][r] = h[32 mb + l32][32 wave + 8 (r>>2) + 4 kh + (r&3)]: + b1, GELU, 16-bit into h(c % 2).
+      // h1[mb][r] = h[32 mb + l32][32 wave + 8 (r>>2) + 4 kh + (r&3)]: + b1, GELU, post, 16-bit into h(c % 2).
       char* hb = hs + (c & 1) * kHBytes;
+      float v[32];  // v[16 mb + r]
+      static_for<0, 2>([&](auto mb) {
+        static_for<0, 4>([&](auto g) {
+          static_for<0, 4>([&](auto e) {
+            const uint32_t bw = (uint32_t)(e < 2 ? bq[g].x : bq[g].y) >> (16 * (e & 1));
+            float t = h1[mb][4 * g + e] + to_f32<T>(bw & 0xffffu);
+            if constexpr (GELU == FUSEML_OP_GELU_TANH)
+              t = gelu_tanh(t);
+            else
+              t = gelu_erf(t);
+            v[16 * mb + 4 * g + e] = t;
+          });
+        });
+      });
+      post_ops<32>(d, v);
       static_for<0, 2>([&](auto mb) {
         const int m = 32 * mb + l32;
         static_for<0, 4>([&](auto g) {
-          float v[4];
-          static_for<0, 4>([&](auto e) {
-            const uint32_t bw = (uint32_t)(e < 2 ? bq[g].x : bq[g].y) >> (16 * (e & 1));
-            v[e] = h1[mb][4 * g + e] + to_f32<T>(bw & 0xffffu);
-            if constexpr (GELU == FUSEML_OP_GELU_TANH)
-              v[e] = gelu_tanh(v[e]);
-            else
-              v[e] = gelu_erf(v[e]);
-          });
-          const i32x2_t hv = {(int)pack2<T>(v[0], v[1]), (int)pack2<T>(v[2], v[3])};
+          constexpr int o = 16 * mb + 4 * g;
+          const i32x2_t hv = {(int)pack2<T>(v[o], v[o + 1]), (int)pack2<T>(v[o + 2], v[o + 3])};
           *reinterpret_cast<i32x2_t*>(hb + h_byte(m, 4 * wave + g, kh)) = hv;
         });
       });
@@ -617,6 +644,16 @@ int validate(const fuseml_mlp_desc* dp) {
   if (d.gelu != FUSEML_OP_GELU_ERF && d.gelu != FUSEML_OP_GELU_TANH) {
     set_error("mlp_block: activation must be GELU (erf or tanh)");
     return FUSEML_EINVAL;
+  }
+  if (d.n_post < 0 || d.n_post > FUSEML_MLP_MAX_POST) {
+    set_error("mlp_block: n_post must be 0 to FUSEML_MLP_MAX_POST");
+    return FUSEML_EINVAL;
+  }
+  for (int p = 0; p < d.n_post; ++p) {
+    if (d.post_kind[p] != FUSEML_OP_SCALE && d.post_kind[p] != FUSEML_OP_ADD_SCALAR) {
+      set_error("mlp_block: post-GELU ops are FUSEML_OP_SCALE and FUSEML_OP_ADD_SCALAR only");
+      return FUSEML_EINVAL;
+    }
   }
   if (!(d.D == 256 || d.D == 512 || d.D == 1024)) {
     set_error("mlp_block: D must be 256, 512 or 1024 (the 64 x D accumulator lives in registers)");

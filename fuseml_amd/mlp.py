@@ -6,11 +6,14 @@ single user (fuseml/passes/fusion_pass.py:203-206) — so the GELU output ``h``
 is written to HBM by the first launch and read back by the second.  With
 ``FuseMLCompiler(fuse_mlp_block=True)`` a pair of groups
 
-    G1: addmm(b1, x, t(W1)) -> gelu                      (h has one user: G2)
+    G1: addmm(b1, x, t(W1)) -> gelu [-> scale / add_scalar ...]   (h has one user: G2)
     G2: addmm(b2, h, t(W2)) -> add(., r)
 
 is bound to one :class:`HipMlpLauncher`, which calls ``fuseml_mlp_block``:
-``h`` stays in LDS chunk by chunk and never reaches HBM.  The kernel holds a
+``h`` stays in LDS chunk by chunk and never reaches HBM.  Up to
+``_abi.MLP_MAX_POST`` scalar ops after the GELU (the reference's
+activation-heavy block, ``gelu(.) * 0.5 + 0.125``, bench_mlp_block.py:185-207)
+run in the kernel too, in order, in fp32.  The kernel holds a
 64 x D fp32 accumulator per row block in registers, so it takes D (the model
 width) of 256, 512 or 1024 only; other pairs keep their two launches.  The
 default ``fuse_mlp_block="auto"`` binds a pair only where the single kernel
@@ -47,6 +50,7 @@ MLP_AUTO_WIDTH = 256
 MLP_AUTO_MIN_ROW_BLOCKS = 256
 
 _DTYPES = {torch.bfloat16: _abi.BF16, torch.float16: _abi.F16}
+_POST_KINDS = {"scale": _abi.OP_SCALE, "add_scalar": _abi.OP_ADD_SCALAR}
 
 
 def mlp_shape_supported(M: int, D: int, I: int, dtype: torch.dtype) -> Tuple[bool, str]:
@@ -99,9 +103,14 @@ class HipMlpLauncher:
     N_INPUTS = 6
 
     def __init__(self, approximate: str = "none", eager_fn: Optional[Callable[..., Any]] = None,
-                 kernel_signature: str = "mlp_block", pack_weights: bool = True) -> None:
+                 kernel_signature: str = "mlp_block", pack_weights: bool = True,
+                 post: Tuple[Tuple[str, float], ...] = ()) -> None:
         self.__name__ = "fuseml_mlp_block"
         self.approximate = approximate
+        # Scalar ops on the GELU's output, in order: ("scale", s) or ("add_scalar", s).
+        if len(post) > _abi.MLP_MAX_POST or any(k not in _POST_KINDS for k, _ in post):
+            raise ValueError(f"post ops: at most {_abi.MLP_MAX_POST} of {sorted(_POST_KINDS)}, got {post!r}")
+        self.post = tuple((k, float(v)) for k, v in post)
         # Where the kernel streams weight fragments (D of 256 or 512, I a
         # multiple of 128), W1 and W2 are repacked once into fragment order
         # (fuseml_mlp_pack_weights: 4*D*I extra bytes, held here) and packed
@@ -123,7 +132,8 @@ class HipMlpLauncher:
         return self._guard.fallback_count if self._guard else 0
 
     def __repr__(self) -> str:
-        return f"HipMlpLauncher(gelu={self.approximate})"
+        post = "".join(f", {k}={v:g}" for k, v in self.post)
+        return f"HipMlpLauncher(gelu={self.approximate}{post})"
 
     def launch(self, x: torch.Tensor, w1t: torch.Tensor, b1: torch.Tensor, w2t: torch.Tensor,
                b2: Optional[torch.Tensor], r: Optional[torch.Tensor]) -> torch.Tensor:
@@ -228,6 +238,9 @@ class HipMlpLauncher:
         d.y, d.ldy = y.data_ptr(), D
         d.dtype = _DTYPES[dt]
         d.gelu = self._gelu
+        d.n_post = len(self.post)
+        for i, (k, v) in enumerate(self.post):
+            d.post_kind[i], d.post_scalar[i] = _POST_KINDS[k], v
         d.wpack = None
         stream = torch.cuda.current_stream(x.device).cuda_stream if x.device.type == "cuda" else 0
         nbytes = 0
@@ -256,15 +269,19 @@ class HipMlpLauncher:
 
 
 def mlp_first_group(spec: EpilogueSpec) -> Optional[Dict[str, Any]]:
-    """G1 = addmm(b1, x, t(W1)) -> gelu: the slots of b1/x/t(W1) and the GELU form."""
-    if spec.reductions or spec.extra_dtypes or not spec.store_tile or len(spec.ops) != 2 \
+    """G1 = addmm(b1, x, t(W1)) -> gelu [-> scale / add_scalar, at most
+    MLP_MAX_POST]: the slots of b1/x/t(W1), the GELU form and the scalar ops."""
+    if spec.reductions or spec.extra_dtypes or not spec.store_tile or not 2 <= len(spec.ops) <= 2 + _abi.MLP_MAX_POST \
             or spec.output_shapes or spec.operand_shapes:
         return None
-    bias, act = spec.ops
+    bias, act, post = spec.ops[0], spec.ops[1], spec.ops[2:]
     if bias.kind != "add" or bias.scalar != 1.0 or act.kind not in ("gelu_erf", "gelu_tanh"):
         return None
+    if any(op.kind not in _POST_KINDS for op in post):
+        return None
     return {"x": spec.left, "w1t": spec.right, "b1": bias.operand,
-            "approximate": "tanh" if act.kind == "gelu_tanh" else "none"}
+            "approximate": "tanh" if act.kind == "gelu_tanh" else "none",
+            "post": tuple((op.kind, float(op.scalar)) for op in post)}
 
 
 def mlp_second_group(spec: EpilogueSpec) -> Optional[Dict[str, Any]]:

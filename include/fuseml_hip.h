@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FUSEML_ABI_VERSION 5
+#define FUSEML_ABI_VERSION 6
 
 #define FUSEML_MAX_OPS 16
 #define FUSEML_MAX_OPERANDS 8
@@ -189,9 +189,13 @@ int fuseml_device_arch(int device, char* buf, int buflen);
 /* ------------------------------------------------------------------------
  * The whole MLP block in one launch (opt-in):
  *
- *     y = GELU(x W1^T + b1) W2^T + b2 + r
+ *     y = post(GELU(x W1^T + b1)) W2^T + b2 + r
  *
- * with h = GELU(x W1^T + b1) kept on chip (never written to HBM).  The
+ * with h = post(GELU(x W1^T + b1)) kept on chip (never written to HBM);
+ * post is up to FUSEML_MLP_MAX_POST scalar ops (FUSEML_OP_SCALE: v * s,
+ * FUSEML_OP_ADD_SCALAR: v + s) applied in order in fp32, as the first
+ * group's epilogue would (the reference's activation-heavy block,
+ * benchmarks/bench_mlp_block.py:185-207, scales and shifts the GELU).  The
  * reference has no counterpart: it runs the block as two launches of its
  * generated kernel (kernel_launcher.py:793-796 / 811-814, once per group),
  * because an addmm ends a fusion group (fuseml/passes/topology.py:63-64) and
@@ -202,6 +206,8 @@ int fuseml_device_arch(int device, char* buf, int buflen);
  * Limits: D in {256, 512, 1024} (the 64 x D fp32 accumulator of a row block
  * lives in registers), I a multiple of 32, all tensors bf16 or all fp16.
  * ------------------------------------------------------------------------ */
+#define FUSEML_MLP_MAX_POST 4
+
 typedef struct fuseml_mlp_desc {
   int64_t M, D, I;
   const void* x;
@@ -222,6 +228,12 @@ typedef struct fuseml_mlp_desc {
    * W1 and W2 as they are).  Used where the kernel streams weight fragments
    * (D of 256 or 512, I a multiple of 128); w1 and w2 are still required. */
   const void* wpack;
+  /* Scalar ops applied to GELU's output before it is rounded to h: kinds
+   * FUSEML_OP_SCALE or FUSEML_OP_ADD_SCALAR, n_post of them (0 to
+   * FUSEML_MLP_MAX_POST). */
+  int32_t n_post;
+  int32_t post_kind[FUSEML_MLP_MAX_POST];
+  float post_scalar[FUSEML_MLP_MAX_POST];
 } fuseml_mlp_desc;
 
 /* Launch the single-kernel MLP block on `stream`.  0 or a FUSEML_E* code. */

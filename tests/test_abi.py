@@ -44,6 +44,7 @@ def test_header_constants_match_binding():
     assert int(defines["FUSEML_MAX_OPS"]) == _abi.MAX_OPS
     assert int(defines["FUSEML_MAX_OPERANDS"]) == _abi.MAX_OPERANDS
     assert int(defines["FUSEML_MAX_EXTRA_OUT"]) == _abi.MAX_EXTRA_OUT
+    assert int(re.search(r"#define FUSEML_MLP_MAX_POST (\d+)", text).group(1)) == _abi.MLP_MAX_POST
 
 
 def _desc(M=256, N=256, K=64):

@@ -74,16 +74,17 @@ def test_preset_traffic_matches_the_c2_table():
 
 
 def test_preset_traffic_activation_heavy_and_stacked():
-    """The activation-heavy block adds two [M, I] round trips to eager only;
-    a stack of blocks keeps the blocks' outputs as intermediates."""
+    """The activation-heavy block adds two [M, I] round trips to eager only
+    (its scale and shift run inside either fused path); a stack of blocks keeps
+    the blocks' outputs as intermediates."""
     bench = _bench()
 
     M, D, I = 16384, 256, 1024
     mlp = bench.preset_traffic("mlp_block", M, D, I, 1)
     act = bench.preset_traffic("activation_heavy", M, D, I, 1)
     assert act["eager_bytes"] - mlp["eager_bytes"] == 2 * 2 * M * I * 2
-    assert act["fused_bytes"] == mlp["fused_bytes"] and "single_kernel_bytes" not in act
-    assert act["fused_eliminated"] > mlp["fused_eliminated"]
+    assert act["fused_bytes"] == mlp["fused_bytes"] and act["single_kernel_bytes"] == mlp["single_kernel_bytes"]
+    assert act["fused_eliminated"] > mlp["fused_eliminated"] and act["single_kernel_eliminated"] == 1.0
     st = bench.preset_traffic("stacked_mlp", M, D, I, 4)
     assert st["eager_bytes"] == 4 * mlp["eager_bytes"] and st["fused_bytes"] == 4 * mlp["fused_bytes"]
     # 4 blocks: compulsory = input + 4 blocks' weights + output

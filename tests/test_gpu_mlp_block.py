@@ -1,7 +1,8 @@
 """GPU parity of the single-kernel MLP block (``fuseml_mlp_block``) against the
 float64 oracle.
 
-``y = GELU(x W1^T + b1) W2^T + b2 + r`` with ``h`` kept on chip.  The kernel
+``y = post(GELU(x W1^T + b1)) W2^T + b2 + r`` with ``h`` kept on chip (post:
+scalar scale/shift ops, the reference's activation-heavy block).  The kernel
 rounds ``h`` to the operand dtype before the second GEMM, as the two-launch
 path (and eager bf16) do.  Cases: every supported width D (256, 512, 1024),
 ragged M (not a multiple of the 64-row block), I down to one 32-column chunk,
@@ -47,9 +48,10 @@ def _inputs(M, D, I, dtype, seed):
     return x, w1, b1, w2, b2, r
 
 
-def _oracle(x, w1, b1, w2, b2, r, approximate="none", dtype=None):
+def _oracle(x, w1, b1, w2, b2, r, approximate="none", dtype=None, post=()):
     h = ora_w.linear(_np(x), _np(w1), _np(b1))
     h = ora.gelu_tanh(h) if approximate == "tanh" else ora.gelu_erf(h)
+    h, _ = ora.apply_chain(h, [(kind, 0, s) for kind, s in post], [])
     y = ora_w.linear(h, _np(w2), None if b2 is None else _np(b2))
     return y if r is None else y + _np(r)
 
@@ -67,6 +69,51 @@ def test_mlp_block_parity(shape, approximate):
     y = HipMlpLauncher(approximate)(x.cuda(), w1.t().cuda(), b1.cuda(), w2.t().cuda(), b2.cuda(), r.cuda())
     torch.cuda.synchronize()
     _close(y, _oracle(x, w1, b1, w2, b2, r, approximate), f"mlp_block {shape} {approximate}")
+
+
+@pytest.mark.parametrize("post", [(("scale", 0.5), ("add_scalar", 0.125)),
+                                  (("add_scalar", -0.25), ("scale", 3.0), ("scale", -0.5), ("add_scalar", 1.0))],
+                         ids=["act_heavy", "four_ops"])
+@pytest.mark.parametrize("shape", [(300, 256, 1024), (129, 512, 96), (64, 1024, 32)], ids=lambda s: "x".join(map(str, s)))
+def test_mlp_block_post_gelu_ops(shape, post):
+    """Scalar ops between the GELU and the second GEMM (the reference's
+    activation-heavy block scales and shifts the GELU), on both kernels."""
+    from fuseml_amd.mlp import HipMlpLauncher
+
+    M, D, I = shape
+    print(f"case mlp_block post ops shape={shape} post={post}", flush=True)
+    x, w1, b1, w2, b2, r = _inputs(M, D, I, torch.bfloat16, seed=7 * M + D + I)
+    y = HipMlpLauncher(post=post)(x.cuda(), w1.t().cuda(), b1.cuda(), w2.t().cuda(), b2.cuda(), r.cuda())
+    torch.cuda.synchronize()
+    _close(y, _oracle(x, w1, b1, w2, b2, r, post=post), f"mlp_block {shape} post {post}")
+
+
+def test_activation_heavy_memory_bound_compiled():
+    """The reference's activation_heavy_memory_bound preset (x[16384,256] ->
+    1024 -> 256) under the default options: one single-kernel launch carrying
+    the block's * 0.5 + 0.125, against the float64 oracle at sampled rows."""
+    from fuseml_amd.compiler import FuseMLCompiler
+    from fuseml_amd.mlp import HipMlpLauncher
+    from fuseml_amd.workloads import reference_preset
+
+    print("case mlp_block compiled activation_heavy_memory_bound", flush=True)
+    wl = reference_preset("activation_heavy_memory_bound")
+    m, x = wl.model, wl.inputs[0]
+    rng = np.random.default_rng(11)
+    rows = np.unique(np.concatenate([[0, 16383], rng.integers(0, 16384, 64)]))
+    xs = x[torch.as_tensor(rows)]
+    ref = _oracle(xs, m.linear1.weight, m.linear1.bias, m.linear2.weight, m.linear2.bias, xs,
+                  post=(("scale", 0.5), ("add_scalar", 0.125)))
+    wl.to("cuda")
+    torch._dynamo.reset()
+    be = FuseMLCompiler()
+    with torch.no_grad():
+        y = torch.compile(wl.model, backend=be)(*wl.inputs)
+    torch.cuda.synchronize()
+    (L,) = be.launchers
+    assert isinstance(L, HipMlpLauncher) and L.launch_count == 1 and L.fallback_count == 0
+    assert L.post == (("scale", 0.5), ("add_scalar", 0.125))
+    _close(y[torch.as_tensor(rows).cuda()], ref, "compiled activation_heavy_memory_bound")
 
 
 def test_mlp_block_fp16_without_bias_and_residual():

@@ -20,7 +20,7 @@ from fuseml_amd import _abi
 from fuseml_amd.compiler import FuseMLCompiler
 from fuseml_amd.fallback import FORCE_FAIL_ENV
 from fuseml_amd.mlp import HipMlpLauncher, mlp_block_beats_two_launches, mlp_shape_supported
-from fuseml_amd.workloads import StackedMLP, TransformerMLP
+from fuseml_amd.workloads import ActivationHeavyMLP, StackedMLP, TransformerMLP
 
 BF = torch.bfloat16
 
@@ -83,6 +83,35 @@ def test_auto_binds_where_the_single_kernel_wins(monkeypatch):
     with torch.no_grad():
         assert torch.equal(_compile(m, be)(x), m(x))
     assert len(be.launchers) == 2 and not any(isinstance(l, HipMlpLauncher) for l in be.launchers)
+
+
+def test_activation_heavy_block_binds_with_its_scalar_ops(monkeypatch):
+    """The reference's activation-heavy block, gelu(linear1(x)) * 0.5 + 0.125
+    into linear2 + x, at the memory_bound shape: one single-kernel launch whose
+    post-GELU ops are the scale and the shift, in graph order."""
+    torch.manual_seed(0)
+    monkeypatch.setenv(FORCE_FAIL_ENV, "1")
+    m = ActivationHeavyMLP(256, 1024).to(BF).eval()
+    x = torch.randn(16384, 256, dtype=BF)
+    be = FuseMLCompiler(require_gfx950=False)
+    with torch.no_grad():
+        assert torch.equal(_compile(m, be)(x), m(x))
+    (L,) = be.launchers
+    assert isinstance(L, HipMlpLauncher) and L.post == (("scale", 0.5), ("add_scalar", 0.125))
+
+
+def test_first_group_matcher_takes_scalar_ops_only():
+    from fuseml_amd.epilogue import EpilogueSpec, EpiOp
+    from fuseml_amd.mlp import mlp_first_group
+
+    base = (EpiOp("add", 0), EpiOp("gelu_erf"))
+    m1 = mlp_first_group(EpilogueSpec(1, 2, base + (EpiOp("scale", scalar=0.5), EpiOp("add_scalar", scalar=0.125)), BF))
+    assert m1 is not None and m1["post"] == (("scale", 0.5), ("add_scalar", 0.125))
+    assert mlp_first_group(EpilogueSpec(1, 2, base, BF))["post"] == ()
+    assert mlp_first_group(EpilogueSpec(1, 2, base + (EpiOp("relu"),), BF)) is None
+    assert mlp_first_group(EpilogueSpec(1, 2, base + (EpiOp("add", 3),), BF)) is None
+    five = base + tuple(EpiOp("scale", scalar=2.0) for _ in range(_abi.MLP_MAX_POST + 1))
+    assert mlp_first_group(EpilogueSpec(1, 2, five, BF)) is None
 
 
 def test_fuse_mlp_block_rejects_unknown_modes():
@@ -155,11 +184,28 @@ def test_mlp_descriptor_from_graph_layouts():
     assert y.shape == (M, D) and y.dtype == BF
     assert (c["M"], c["D"], c["I"], c["ldx"], c["ldw1"], c["ldw2"], c["ldr"], c["ldy"]) == (M, D, I, D, D, I, D, D)
     assert c["x"] == x.data_ptr() and c["r"] == x.data_ptr() and c["w1"] == w1.data_ptr()
-    assert c["dtype"] == _abi.BF16 and c["gelu"] == _abi.OP_GELU_TANH
+    assert c["dtype"] == _abi.BF16 and c["gelu"] == _abi.OP_GELU_TANH and c["n_post"] == 0
     with pytest.raises(ValueError):
         L(x, w1.t(), b1)
     with pytest.raises(_abi.FuseMLHipError):   # shapes that do not chain
         L(x, w1.t(), b1, w1.t(), b2, x)
+
+
+def test_mlp_descriptor_carries_the_scalar_ops():
+    M, D, I = 16, 256, 128
+    x = torch.randn(M, D, dtype=BF)
+    w1, b1, w2 = torch.randn(I, D, dtype=BF), torch.randn(I, dtype=BF), torch.randn(D, I, dtype=BF)
+    L = HipMlpLauncher(post=(("scale", 0.5), ("add_scalar", 0.125)))
+    rec = _Recorder()
+    L._lib = rec
+    L(x, w1.t(), b1, w2.t(), None, None)
+    (c,) = rec.calls
+    assert c["n_post"] == 2 and list(c["post_kind"])[:2] == [_abi.OP_SCALE, _abi.OP_ADD_SCALAR]
+    assert list(c["post_scalar"])[:2] == [0.5, 0.125]
+    with pytest.raises(ValueError):
+        HipMlpLauncher(post=(("relu", 0.0),))
+    with pytest.raises(ValueError):
+        HipMlpLauncher(post=(("scale", 2.0),) * (_abi.MLP_MAX_POST + 1))
 
 
 def test_mlp_shape_rule():
