@@ -116,6 +116,24 @@ def test_activation_heavy_memory_bound_compiled():
     _close(y[torch.as_tensor(rows).cuda()], ref, "compiled activation_heavy_memory_bound")
 
 
+@pytest.mark.parametrize("shape", [(300, 256, 1024), (129, 512, 384)], ids=lambda s: "x".join(map(str, s)))
+def test_mlp_block_unpacked_weights(shape):
+    """The I-split kernel reading W1 and W2 as they are (no repacked copy: a
+    C-ABI caller that passes no wpack) against the oracle and bitwise against
+    the packed path (the same fragments in the same order)."""
+    from fuseml_amd.mlp import HipMlpLauncher
+
+    M, D, I = shape
+    print(f"case mlp_block unpacked shape={shape}", flush=True)
+    x, w1, b1, w2, b2, r = _inputs(M, D, I, torch.bfloat16, seed=3 * M + D + I)
+    args = (x.cuda(), w1.t().cuda(), b1.cuda(), w2.t().cuda(), b2.cuda(), r.cuda())
+    y = HipMlpLauncher(pack_weights=False)(*args)
+    yp = HipMlpLauncher()(*args)
+    torch.cuda.synchronize()
+    _close(y, _oracle(x, w1, b1, w2, b2, r), f"mlp_block unpacked {shape}")
+    assert torch.equal(y, yp)
+
+
 def test_mlp_block_fp16_without_bias_and_residual():
     from fuseml_amd.mlp import HipMlpLauncher
 
