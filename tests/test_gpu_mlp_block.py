@@ -134,6 +134,33 @@ def test_mlp_block_unpacked_weights(shape):
     assert torch.equal(y, yp)
 
 
+@pytest.mark.parametrize("mode", [False, True], ids=["two_launches", "single_kernel"])
+def test_activation_heavy_block_compiled_both_paths(mode):
+    """The activation-heavy block (gelu(.) * 0.5 + 0.125 between the GEMMs) at
+    M = 1000 (ragged, below the auto rule's row blocks) through the compiler
+    with two fused launches and forced onto the single kernel."""
+    from fuseml_amd.compiler import FuseMLCompiler
+    from fuseml_amd.mlp import HipMlpLauncher
+    from fuseml_amd.workloads import ActivationHeavyMLP
+
+    print(f"case activation-heavy block compiled fuse_mlp_block={mode}", flush=True)
+    torch.manual_seed(4)
+    m = ActivationHeavyMLP(256, 1024).to(torch.bfloat16).eval()
+    x = torch.randn(1000, 256, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    ref = _oracle(x, m.linear1.weight, m.linear1.bias, m.linear2.weight, m.linear2.bias, x,
+                  post=(("scale", 0.5), ("add_scalar", 0.125)))
+    m, xd = m.to("cuda"), x.cuda()
+    torch._dynamo.reset()
+    be = FuseMLCompiler(fuse_mlp_block=mode, min_output_elements=0)
+    with torch.no_grad():
+        y = torch.compile(m, backend=be)(xd)
+    torch.cuda.synchronize()
+    singles = [L for L in be.launchers if isinstance(L, HipMlpLauncher)]
+    assert be.fusion_strategy == "hip" and len(singles) == (1 if mode else 0)
+    assert len(be.launchers) == (1 if mode else 2)
+    _close(y, ref, f"activation-heavy compiled fuse_mlp_block={mode}")
+
+
 def test_mlp_block_fp16_without_bias_and_residual():
     from fuseml_amd.mlp import HipMlpLauncher
 
