@@ -31,7 +31,8 @@ Rank 0 prints one JSON line carrying:
   harness times it (events around one forward, a synchronisation after each,
   median), eager against ``torch.compile(backend=FuseMLCompiler())`` with the
   default cost model, against every group fused (cost model off) and against
-  the single-kernel MLP block where it applies, with a correctness gate
+  the single-kernel MLP block where it applies, and against the default
+  options replayed from a HIP graph (``hip_graph=True``), with a correctness gate
   (atol 5e-2, rtol 2e-2 against a float32 forward, the reference's gate) and
   the whole-forward HBM bytes of each path counted from the shapes;
 * ``fp32_block`` — the C2 block in fp32 (not a benchmark config): compiled,
@@ -475,6 +476,8 @@ def _presets(args, dev):
                                                        min_output_elements=0, fuse_mlp_block=False)}
             paths["single_kernel_mlp"] = dict(fuse_mlp_block=True, k_per_epilogue_pass=0, min_tiles_long_k=0,
                                               min_output_elements=0)
+            # the default options, replayed from a HIP graph (static outputs)
+            paths["compiled_hip_graph"] = dict(hip_graph=True)
             for label, kw in paths.items():
                 torch._dynamo.reset()
                 be = FuseMLCompiler(**kw)
@@ -485,6 +488,10 @@ def _presets(args, dev):
                 if label == "single_kernel_mlp" and n_mlp == 0:
                     continue
                 r = _time_sync(lambda: c(x), args)
+                if be.graph_forwards:
+                    y = c(x)  # gate a replayed output (the first calls run without the graph)
+                    torch.cuda.synchronize()
+                    r["hip_graph_replays"] = sum(g.replays for g in be.graph_forwards)
                 r.update(check=gate(y), fusion_strategy=be.fusion_strategy,
                          fused_launchers=len({id(L) for L in be.launchers}), dispatch=be.dispatch[:1],
                          speedup_vs_eager=round(res["eager"]["median_ms"] / r["median_ms"], 3))

@@ -344,8 +344,14 @@ class FuseMLCompiler:
                  min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
                  min_tiles_long_k: int = MIN_TILES_LONG_K,
                  k_per_epilogue_pass: int = K_PER_EPILOGUE_PASS,
-                 require_gfx950: bool = True, direct_dispatch: bool = True) -> None:
+                 require_gfx950: bool = True, direct_dispatch: bool = True, hip_graph: bool = False) -> None:
         self.registry = registry
+        # Replay each directly dispatched, static-shape forward from a HIP graph
+        # (fuseml_amd.graphs.HipGraphForward: the returned tensors are static
+        # outputs, overwritten by the next call, as with CUDA graphs under
+        # torch.compile(mode="reduce-overhead")).  Off by default.
+        self.hip_graph = hip_graph
+        self.graph_forwards: List[Any] = []
         # Return the fused graph's forward to Dynamo without AOTAutograd's
         # runtime wrapper when that wrapper would only call it
         # (aot_wrapper_is_identity); `dispatch` records which path each
@@ -402,8 +408,24 @@ class FuseMLCompiler:
         if not ok:
             self.dispatch.append(f"aot: {why}")
             return compiled
-        self.dispatch.append("direct")
-        return _direct_forward(captured["fwd"], params_flat)
+        forward = _direct_forward(captured["fwd"], params_flat)
+        if not self.hip_graph:
+            self.dispatch.append("direct")
+            return forward
+        from .graphs import HipGraphForward, static_shapes
+
+        if not static_shapes(params_flat + list(example_inputs)):
+            self.dispatch.append("direct (no HIP graph: dynamic shapes or inputs off one GPU)")
+            return forward
+        # The graph's parameter and buffer inputs (AOTAutograd's
+        # static_input_indices, over the lifted parameters and then the call's
+        # arguments) are read in place; the other arguments are copied.
+        n_p = len(params_flat)
+        static = {i - n_p for i in getattr(captured["meta"], "static_input_indices", []) if i >= n_p}
+        graph_forward = HipGraphForward(forward, static, params=params_flat)
+        self.graph_forwards.append(graph_forward)
+        self.dispatch.append("direct+hip_graph")
+        return graph_forward
 
     # ------------------------------------------------------------------
     def _device_ok(self, inputs: List[Any]) -> bool:
