@@ -100,14 +100,15 @@ class HipGraphForward:
         self.captures += 1
 
     def __call__(self, *args: torch.Tensor) -> Any:
+        if self._graph is not None and self._stamps(args) != self._stamp:
+            # a weight changed: this call without the graph (it also refreshes
+            # what launchers derive from weights), the next captures again
+            self._graph, self._outputs = None, None
+            self._calls = self._warmup - 1
         if self._graph is not None and self._alias and any(args[i].data_ptr() != p for i, p in self._alias_ptrs):
             # an activation at another address: from now on over private buffers
             self._alias = False
             self._capture(args)
-        if self._graph is not None and self._stamps(args) != self._stamp:
-            # a weight changed: this call without the graph, the next captures again
-            self._graph, self._outputs = None, None
-            self._calls = self._warmup - 1
         if self._graph is None:
             self._calls += 1
             if self._calls <= self._warmup:
