@@ -1,7 +1,7 @@
 """The drop-in boundary with the reference's own FusionGroup (CPU, no kernel launch).
 
-INTEGRATION route B: the reference keeps its compiler, discovery and surgery
-and calls ``build_hip_launcher(group)`` where it built a Triton or cuBLASLt
+The integration route in which the reference keeps its compiler, discovery
+and surgery and calls ``build_hip_launcher(group)`` where it built a Triton or cuBLASLt
 launcher (fuseml/compiler.py:343-409).  The groups it hands over carry only
 the ten fields of fuseml/fusion_group.py:74-85, their nodes are erased by the
 time the launcher is built, and later groups' ``node_args_snapshot`` still
