@@ -224,7 +224,7 @@ def test_c5_four_blocks_chained():
 
 
 @pytest.mark.parametrize("cublas", [False, True], ids=["triton", "cublas_epilogue"])
-def test_route_b_reference_groups_on_gpu(cublas):
+def test_reference_route_reference_groups_on_gpu(cublas):
     from torch.fx.experimental.proxy_tensor import make_fx
 
     from fuseml_amd.compiler import build_hip_launcher
@@ -232,7 +232,7 @@ def test_route_b_reference_groups_on_gpu(cublas):
     from fuseml_amd.workloads import c2_mlp_block
     from refsurgery import bind, reference_groups, reference_surgery
 
-    _case(f"route B reference groups cublas={cublas}")
+    _case(f"reference-route groups cublas={cublas}")
     wl = c2_mlp_block(scale=1 / 8)  # x[2048, 1024]
     m = wl.model
     x = wl.inputs[0]
@@ -249,7 +249,7 @@ def test_route_b_reference_groups_on_gpu(cublas):
         y = gm(xd)
     torch.cuda.synchronize()
     assert [b.launch_count for b in bound] == [1, 1] and [b.fallback_count for b in bound] == [0, 0]
-    _close(y, ref, "route B C2 block")
+    _close(y, ref, "reference-route C2 block")
 
 
 # ---------------------------------------------------------------------------

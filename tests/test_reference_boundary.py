@@ -50,7 +50,7 @@ def test_refgroup_has_exactly_the_reference_fields():
 
 
 @pytest.mark.parametrize("cublas", [False, True], ids=["triton", "cublas_epilogue"])
-def test_route_b_mlp_block(monkeypatch, cublas):
+def test_reference_route_mlp_block(monkeypatch, cublas):
     torch.manual_seed(0)
     m = TransformerMLP(64, 256).to(BF).eval()
     x = torch.randn(32, 64, dtype=BF)
@@ -73,7 +73,7 @@ def test_route_b_mlp_block(monkeypatch, cublas):
     assert [b.fallback_count for b in bound] == [1, 1]
 
 
-def test_route_b_stacked_blocks(monkeypatch):
+def test_reference_route_stacked_blocks(monkeypatch):
     torch.manual_seed(1)
     m = StackedMLP(64, 128, 3).to(BF).eval()
     x = torch.randn(16, 64, dtype=BF)
@@ -84,7 +84,7 @@ def test_route_b_stacked_blocks(monkeypatch):
         assert torch.equal(gm(x), m(x))
 
 
-def test_route_b_activation_heavy_role_bias(monkeypatch):
+def test_reference_route_activation_heavy_role_bias(monkeypatch):
     torch.manual_seed(0)
     m = ActivationHeavy(64, 128).to(BF).eval()
     with torch.no_grad():
@@ -107,7 +107,7 @@ def _absorb(gm, group, node):
     group.node_args_snapshot[node.name] = tuple(node.args)
 
 
-def test_route_b_escape_returns_tuple(monkeypatch):
+def test_reference_route_escape_returns_tuple(monkeypatch):
     """A group whose middle node is also used outside (the reference's escape
     analysis, fusion_pass.py:300-329): the launcher returns (primary, escape)."""
     def f(x, w):
@@ -137,7 +137,7 @@ def test_route_b_escape_returns_tuple(monkeypatch):
     assert torch.equal(y, ry) and torch.equal(h, rh)
 
 
-def test_route_b_full_reduction_gets_eager_closure():
+def test_reference_route_full_reduction_gets_eager_closure():
     """torch.amax(relu(x @ w)): a reduction over every element is no tile axis.
     The reference fuses it as a per-row amax; here the group is bound to its
     eager nodes and the 0-d result is right."""
@@ -158,7 +158,7 @@ def test_route_b_full_reduction_gets_eager_closure():
     assert out.shape == () and torch.equal(out, f(x, w))
 
 
-def test_route_b_square_permute_gets_eager_closure():
+def test_reference_route_square_permute_gets_eager_closure():
     def f(x, w):
         return torch.relu((x @ w).T)
 
