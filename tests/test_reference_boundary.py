@@ -37,7 +37,7 @@ def trace(model, *inputs):
         return make_fx(model)(*inputs)
 
 
-def route_b(model, inputs, cublas=False):
+def reference_route(model, inputs, cublas=False):
     gm = trace(model, *inputs)
     groups = reference_groups(gm, inputs, cublas=cublas)
     phs = reference_surgery(gm, groups)
@@ -54,7 +54,7 @@ def test_reference_route_mlp_block(monkeypatch, cublas):
     torch.manual_seed(0)
     m = TransformerMLP(64, 256).to(BF).eval()
     x = torch.randn(32, 64, dtype=BF)
-    gm, groups, bound = route_b(m, (x,), cublas=cublas)
+    gm, groups, bound = reference_route(m, (x,), cublas=cublas)
     assert all(isinstance(b, HipKernelLauncher) for b in bound)
     assert [b.spec.describe() for b in bound] == ["gemm(1,2) -> add[0] -> gelu_erf",
                                                   "gemm(1,2) -> add[0] -> add[3]"]
@@ -77,7 +77,7 @@ def test_reference_route_stacked_blocks(monkeypatch):
     torch.manual_seed(1)
     m = StackedMLP(64, 128, 3).to(BF).eval()
     x = torch.randn(16, 64, dtype=BF)
-    gm, groups, bound = route_b(m, (x,))
+    gm, groups, bound = reference_route(m, (x,))
     assert len(bound) == 6 and all(isinstance(b, HipKernelLauncher) for b in bound)
     monkeypatch.setenv(FORCE_FAIL_ENV, "1")
     with torch.no_grad():
@@ -90,7 +90,7 @@ def test_reference_route_activation_heavy_role_bias(monkeypatch):
     with torch.no_grad():
         m.row.uniform_(-0.5, 0.5)
     x, g = torch.randn(32, 64, dtype=BF), torch.rand(32, 128, dtype=BF)
-    gm, groups, bound = route_b(m, (x, g))
+    gm, groups, bound = reference_route(m, (x, g))
     (b,) = bound
     assert b.spec.describe() == "gemm(1,2) -> add[0] -> relu -> mul[3] -> sigmoid -> add[4]"
     monkeypatch.setenv(FORCE_FAIL_ENV, "1")
