@@ -80,6 +80,38 @@ def test_graph_reads_a_refilled_input_in_place():
     assert all(torch.equal(a, b) for a, b in zip(got, want))
 
 
+def test_graph_with_fused_row_reductions():
+    """C4's module at 1/8 of its rows with sibling reductions fused: the sum,
+    amax and mean outputs are initialised inside the graph (fill kernels) and
+    accumulated by the kernel's atomics on every replay.  Sums and means are
+    compared with a tolerance (atomic order), the tile and the amax bitwise."""
+    from fuseml_amd.workloads import c4_gemm_row_reductions
+
+    print("case hip_graph fused row reductions (C4 at 1/8)", flush=True)
+    wl = c4_gemm_row_reductions(scale=1 / 8).to("cuda")
+    m, x0 = wl.model, wl.inputs[0]
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    xs = [torch.randn(x0.shape, generator=gen, device="cuda").to(x0.dtype) for _ in range(5)]
+    buf = torch.empty_like(x0)
+    with torch.no_grad():
+        plain, _ = _compiled(m, fuse_sibling_reductions=True, min_tiles_long_k=0)
+        want = [tuple(t.clone() for t in plain(x)) for x in xs]
+        graphed, be = _compiled(m, fuse_sibling_reductions=True, min_tiles_long_k=0, hip_graph=True)
+        got = []
+        for x in xs:
+            buf.copy_(x)
+            got.append(tuple(t.clone() for t in graphed(buf)))
+        torch.cuda.synchronize()
+    assert be.dispatch == ["direct+hip_graph"] and be.graph_forwards[0].captures == 1
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert len(g) == len(w)
+        for a, b in zip(g, w):
+            if a.dtype == torch.float32 and a.dim() == 1:
+                assert torch.allclose(a, b, rtol=1e-5, atol=1e-3), f"call {i}: reduction differs"
+            else:
+                assert torch.equal(a, b), f"call {i}: output differs"
+
+
 def test_weight_change_recaptures():
     from fuseml_amd.workloads import reference_preset
 
