@@ -20,7 +20,10 @@ Semantics, as ``torch.compile(mode="reduce-overhead")``'s CUDA graphs:
   new version counter) runs once without the graph and captures it again on
   the following call, so results always follow the current weights;
 * the first ``warmup`` calls run without the graph (they build the launchers'
-  plans and the single-kernel MLP's packed weights outside the capture).
+  plans and the single-kernel MLP's packed weights outside the capture);
+* a forward that cannot be captured (an operation the stream capture refuses)
+  is run without the graph from then on, with a warning: the capture error is
+  not raised to the caller.
 
 Only graphs with static shapes on one GPU are captured (the compiler checks);
 the graph replays on the caller's current stream.  The reference has no
@@ -30,6 +33,7 @@ kernel_launcher.py:640-821).
 
 from __future__ import annotations
 
+import warnings
 from typing import Any, Callable, List, Optional, Sequence, Set
 
 import torch
@@ -76,12 +80,15 @@ class HipGraphForward:
         self._stamp: List[tuple] = []
         self.captures = 0
         self.replays = 0
+        # Set when a capture failed: every later call runs fwd without a graph.
+        self.capture_error: Optional[str] = None
 
     def _stamps(self, args: Sequence[torch.Tensor]) -> List[tuple]:
         return [(args[i].data_ptr(), args[i]._version) for i in self._static_list] + \
                [(p.data_ptr(), p._version) for p in self._params]
 
-    def _capture(self, args: Sequence[torch.Tensor]) -> None:
+    def _capture(self, args: Sequence[torch.Tensor]) -> bool:
+        """Capture fwd over ``args`` (or private copies); False if the capture failed."""
         self._graph = None
         dynamic = [i for i in range(len(args)) if i not in self._static_args]
         if self._alias:
@@ -93,13 +100,23 @@ class HipGraphForward:
         call = [a if b is None else b for a, b in zip(args, self._bufs)]
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            out = self._fwd(*call)
+        try:
+            with torch.cuda.graph(g):
+                out = self._fwd(*call)
+        except Exception as exc:  # noqa: BLE001 - any capture failure: keep the plain forward
+            self._graph, self._outputs, self._bufs = None, None, []
+            self.capture_error = f"{type(exc).__name__}: {exc}"
+            warnings.warn(f"fuseml: HIP-graph capture failed, running the forward without a graph "
+                          f"({self.capture_error})", RuntimeWarning, stacklevel=3)
+            return False
         self._graph, self._outputs = g, out
         self._stamp = self._stamps(args)
         self.captures += 1
+        return True
 
     def __call__(self, *args: torch.Tensor) -> Any:
+        if self.capture_error is not None:
+            return self._fwd(*args)
         if self._graph is not None and self._stamps(args) != self._stamp:
             # a weight changed: this call without the graph (it also refreshes
             # what launchers derive from weights), the next captures again
@@ -108,12 +125,12 @@ class HipGraphForward:
         if self._graph is not None and self._alias and any(args[i].data_ptr() != p for i, p in self._alias_ptrs):
             # an activation at another address: from now on over private buffers
             self._alias = False
-            self._capture(args)
+            if not self._capture(args):
+                return self._fwd(*args)
         if self._graph is None:
             self._calls += 1
-            if self._calls <= self._warmup:
+            if self._calls <= self._warmup or not self._capture(args):
                 return self._fwd(*args)
-            self._capture(args)
         for a, b in zip(args, self._bufs):
             if b is not None:
                 b.copy_(a)

@@ -2,6 +2,7 @@
 state machine with a stand-in graph object (no device), and the compiler's
 hip_graph option declining a graph off the GPU."""
 
+import pytest
 import torch
 
 import fuseml_amd.compiler as comp
@@ -99,6 +100,29 @@ def test_replaced_weight_storage_recaptures(monkeypatch):
     assert torch.equal(f(w1, x), w1 * x) and f.captures == 1
     assert torch.equal(f(w2, x), w2 * x) and f.captures == 1   # another storage: plain call
     assert torch.equal(f(w2, x), w2 * x) and f.captures == 2
+
+
+def test_capture_failure_keeps_the_plain_forward(monkeypatch):
+    """An operation the stream capture refuses: a warning, the call's result
+    from the plain forward, and no further capture attempts."""
+    _patch(monkeypatch)
+    calls = []
+
+    def fwd(w, x):
+        calls.append("run")
+        if _FakeGraph.current is not None:
+            raise RuntimeError("operation not permitted when stream is capturing")
+        return w * x
+
+    w, x = torch.full((4,), 2.0), torch.ones(4)
+    f = graphs.HipGraphForward(fwd, static_args={0}, warmup=1)
+    assert torch.equal(f(w, x), w * x) and f.capture_error is None
+    with pytest.warns(RuntimeWarning, match="capture failed"):
+        y = f(w, x)
+    assert torch.equal(y, w * x) and f.captures == 0 and "not permitted" in f.capture_error
+    n = len(calls)
+    x.fill_(3.0)
+    assert torch.equal(f(w, x), w * x) and len(calls) == n + 1 and f.captures == 0
 
 
 def test_static_shapes_rule():
