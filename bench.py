@@ -34,7 +34,10 @@ Rank 0 prints one JSON line carrying:
   the single-kernel MLP block where it applies, and against the default
   options replayed from a HIP graph (``hip_graph=True``), with a correctness gate
   (atol 5e-2, rtol 2e-2 against a float32 forward, the reference's gate) and
-  the whole-forward HBM bytes of each path counted from the shapes;
+  the whole-forward HBM bytes of each path counted from the shapes; each path
+  also timed on the device alone (20 forwards captured into one HIP graph and
+  replayed: no host dispatch in the time), with its TFLOP/s and compulsory-byte
+  GB/s against the bf16 MFMA and HBM specs (``device``);
 * ``fp32_block`` — the C2 block in fp32 (not a benchmark config): compiled,
   both groups as bf16 split products, against eager fp32, with errors
   against float64 at sampled rows;
@@ -444,6 +447,52 @@ def _time_sync(fn, args, warmup=25):
     return _quartiles(times)
 
 
+def _device_ms(fn, reps=20, repeats=7):
+    """GPU time per fn() call with the host's dispatch out of the measurement:
+    ``reps`` calls captured back to back into one HIP graph, which is replayed
+    between an event pair; median over ``repeats`` replays.  The calls' inputs
+    stay as they are (warm caches, as in the per-call timing)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(repeats):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        g.replay()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e) / reps)
+    del g
+    return statistics.median(times)
+
+
+def preset_roofline(ms: float, flops: float, compulsory_bytes: int) -> dict:
+    """A forward's device time against both rooflines: its flops over the bf16
+    MFMA spec and its compulsory bytes (input, weights, output) over the HBM
+    spec.  ``bound`` names the roofline whose floor is the longer one: a
+    shape whose flops per compulsory byte exceed the ridge point (2.5 PFLOP/s /
+    8 TB/s = 312.5) cannot reach the HBM rate even at full MFMA speed."""
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbps = compulsory_bytes / (ms * 1e-3) / 1e9
+    floor_mfma = flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3
+    floor_hbm = compulsory_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
+    return {"device_ms": round(ms, 4), "tflops": round(tflops, 1), "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "GBps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBS, 4),
+            "bound": "mfma" if floor_mfma >= floor_hbm else "hbm",
+            "frac_of_bound": round(max(floor_mfma, floor_hbm) / ms, 4)}
+
+
 def _presets(args, dev):
     """The reference's presets: eager, compiled (default cost model), every group
     fused, and the single-kernel MLP block, timed and checked the reference's way."""
@@ -471,6 +520,8 @@ def _presets(args, dev):
 
             res["eager"] = _time_sync(lambda: m(x), args)
             res["eager"]["check"] = gate(m(x))
+            comp_bytes = res["traffic"]["compulsory_bytes"]
+            res["eager"]["device"] = preset_roofline(_device_ms(lambda: m(x)), wl.flops, comp_bytes)
             # all_fused: every group as its own launch (no single-kernel MLP)
             paths = {"compiled": {}, "all_fused": dict(k_per_epilogue_pass=0, min_tiles_long_k=0,
                                                        min_output_elements=0, fuse_mlp_block=False)}
@@ -495,6 +546,10 @@ def _presets(args, dev):
                 r.update(check=gate(y), fusion_strategy=be.fusion_strategy,
                          fused_launchers=len({id(L) for L in be.launchers}), dispatch=be.dispatch[:1],
                          speedup_vs_eager=round(res["eager"]["median_ms"] / r["median_ms"], 3))
+                if not be.graph_forwards:  # a HIP-graph forward is not captured inside another graph
+                    dv = preset_roofline(_device_ms(lambda: c(x)), wl.flops, comp_bytes)
+                    dv["speedup_vs_eager"] = round(res["eager"]["device"]["device_ms"] / dv["device_ms"], 3)
+                    r["device"] = dv
                 r["single_kernel_launchers"] = n_mlp
                 res[label] = r
         out[name] = res

@@ -89,3 +89,24 @@ def test_preset_traffic_activation_heavy_and_stacked():
     assert st["eager_bytes"] == 4 * mlp["eager_bytes"] and st["fused_bytes"] == 4 * mlp["fused_bytes"]
     # 4 blocks: compulsory = input + 4 blocks' weights + output
     assert st["compulsory_bytes"] == (2 * M * D + 4 * (2 * D * I + I + D)) * 2
+
+
+def test_preset_roofline_names_the_binding_roofline():
+    """Both fractions from one device time; the bound is the roofline with the
+    longer floor, which changes sides at 312.5 flops per compulsory byte (the
+    2.5 PFLOP/s : 8 TB/s ridge)."""
+    bench = _bench()
+    B = 10 ** 6
+    above = bench.preset_roofline(0.1, 320.0 * B, B)
+    below = bench.preset_roofline(0.1, 300.0 * B, B)
+    assert above["bound"] == "mfma" and below["bound"] == "hbm"
+    assert above["tflops"] == 3.2 and above["frac_mfma"] == round(3.2 / 2500.0, 4)
+    assert above["GBps"] == 10.0 and above["frac_hbm"] == round(10.0 / 8000.0, 4)
+    # frac_of_bound = the bound's floor over the measured time
+    assert abs(above["frac_of_bound"] - 320.0 * B / 2.5e15 / 1e-4) <= 1e-4
+    assert abs(below["frac_of_bound"] - B / 8e12 / 1e-4) <= 1e-4
+    # the reference's memory_bound preset (16384 rows, 256 -> 1024) is MFMA-bound on this GPU
+    M, D, I = 16384, 256, 1024
+    t = bench.preset_traffic("mlp_block", M, D, I, 1)
+    r = bench.preset_roofline(0.03, 2 * 2.0 * M * D * I, t["compulsory_bytes"])
+    assert r["bound"] == "mfma"
