@@ -256,7 +256,7 @@ def load_library() -> ctypes.CDLL:
         return lib
 
 
-VARIANTS = ("large", "deep", "deep3", "small")
+VARIANTS = ("large", "deep", "deep3", "small", "narrow64", "narrow32")
 
 
 def force_variant(name: Optional[str]) -> None:

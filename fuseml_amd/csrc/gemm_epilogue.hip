@@ -60,11 +60,11 @@ constexpr int64_t kTileSpan = 256;  // largest tile edge of any variant
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Pinned variant: 0 automatic, else 1 + index into {large, deep, deep3, small,
-// deep3-generic} (the last: deep3 with the generic op loop even where a fixed
-// chain matches).  Initialised once per process from FUSEML_HIP_TILE, changed
+// deep3-generic, narrow64, narrow32} (deep3-generic: deep3 with the generic op
+// loop even where a fixed chain matches).  Initialised once per process from FUSEML_HIP_TILE, changed
 // only through fuseml_gemm_epilogue_force_variant.
-constexpr const char* kVariantNames[] = {"large", "deep", "deep3", "small", "deep3-generic"};
-constexpr int kNumVariantNames = 5;
+constexpr const char* kVariantNames[] = {"large", "deep", "deep3", "small", "deep3-generic", "narrow64", "narrow32"};
+constexpr int kNumVariantNames = 7;
 constexpr int kForcedDeep3Generic = 5;
 std::atomic<int> g_forced_variant{-1};  // -1: environment not read yet
 
@@ -88,6 +88,31 @@ int forced_variant() {
 
 int match_fixed_chain(const fuseml_gemm_desc& d);
 
+// Below one round of 256-wide tiles, one of the lock-step variants (128x128,
+// 64x128, 32x128): the one whose busiest CU fetches the fewest operand bytes
+// per unit of K, ceil(tiles / CUs) x (BM + BN) rows, the larger tile on a tie.
+// Each CU moves its tiles' A and W rows through the LDS DMA at a roughly fixed
+// rate (37-48 GB/s measured, whatever the tile), so below two 128x128 tiles
+// per CU a narrower tile spreads the same K over more CUs.  Measured (bias +
+// GELU or bias + residual, M x N x K): 128x1024x256 9.6 -> 5.9 us and
+// 1024x1024x1024 16.8 -> 9.9 us on 32x128 tiles; 2048x1024x4096 44 -> 31 us
+// on 64x128 tiles (32x128 tiles, two per CU there, take 35); 2048x4096x1024
+// stays on 128x128 tiles (30.6 us; 64x128 33, 32x128 44).
+TileConfig choose_lockstep(const fuseml_gemm_desc& d, int cus) {
+  const TileConfig* cand[3] = {&kSmall, &kNarrow64, &kNarrow32};
+  const TileConfig* best = cand[0];
+  int64_t best_rows = 0;
+  for (const TileConfig* c : cand) {
+    const int64_t tiles = cdiv(d.M, c->bm) * cdiv(d.N, c->bn);
+    const int64_t rows = cdiv(tiles, cus) * (c->bm + c->bn);
+    if (c == cand[0] || rows < best_rows) {
+      best = c;
+      best_rows = rows;
+    }
+  }
+  return *best;
+}
+
 // `cus`: the device's CU count (the 256-wide variants run one workgroup per CU).
 // `d` has its flags derived (derive_flags).
 TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
@@ -99,6 +124,8 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
     case 3: return d.K % 64 == 0 ? kDeep3 : kDeep;
     case 4: return kSmall;
     case kForcedDeep3Generic: return d.K % 64 == 0 ? kDeep3 : kDeep;
+    case 6: return kNarrow64;
+    case 7: return kNarrow32;
     default: break;
   }
   // A 256x256 tile keeps the LDS traffic per MFMA low enough for the MFMA pipe
@@ -117,7 +144,7 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
   // CU (4 x large_tiles <= 2 x cus): at 128 large tiles on 256 CUs it is 7-17%
   // faster (bias+GELU at K = 512-1024), from 144 on the 256-wide one is.
   const int64_t large_tiles = cdiv(d.M, 256) * cdiv(d.N, 256);
-  if (2 * large_tiles <= cus) return kSmall;
+  if (2 * large_tiles <= cus) return choose_lockstep(d, cus);
   if (d.K % 64 == 0 && (d.K >= 8192 || (d.K >= 2048 && large_tiles >= cus))) return kDeep3;
   if (d.K % 64 == 0 && d.K >= 1024 && large_tiles >= cus) {
     const int ch = match_fixed_chain(d);
@@ -491,7 +518,7 @@ int fuseml_gemm_epilogue_force_variant(const char* name) {
   g_last_error[0] = '\0';
   const int v = variant_code(name);
   if (v < 0) {
-    set_error("unknown variant '%s' (large, deep, deep3, small, deep3-generic or auto)", name);
+    set_error("unknown variant '%s' (large, deep, deep3, small, deep3-generic, narrow64, narrow32 or auto)", name);
     return FUSEML_EINVAL;
   }
   forced_variant();  // the environment is read first, so it cannot override this later
@@ -556,6 +583,10 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
     e = launch_variant<kLarge>(d, stream, cus);
   else if (c.sched == kDeep3.sched)
     e = launch_variant<kDeep3>(d, stream, cus);
+  else if (c.bm == kNarrow64.bm)
+    e = launch_variant<kNarrow64>(d, stream, 0);
+  else if (c.bm == kNarrow32.bm)
+    e = launch_variant<kNarrow32>(d, stream, 0);
   else
     e = launch_variant<kSmall>(d, stream, 0);
   if (e != hipSuccess) {

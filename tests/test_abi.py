@@ -98,9 +98,27 @@ def test_tile_config_choice():
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_bias_gelu(_desc(16384, 4096, 1024))), cfg) == 0
     assert tuple(cfg[:3]) == (256, 256, 8)
     assert 128 * 1024 <= cfg[3] <= 160 * 1024
-    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(64, 512, 2048)), cfg) == 0
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(2048, 4096, 1024)), cfg) == 0
     assert tuple(cfg[:3]) == (128, 128, 4)
     assert 2 * cfg[3] <= 160 * 1024  # two workgroups share one gfx950 CU's LDS
+
+
+@pytest.mark.parametrize("shape,tile", [
+    ((2048, 4096, 1024), (128, 128)),  # 512 tiles: two per CU; narrower tiles only add rows per CU
+    ((2048, 1024, 4096), (64, 128)),   # 128 tiles of 128x128: 256 of 64x128, one per CU
+    ((1024, 1024, 1024), (32, 128)),   # 64 tiles of 128x128: 256 of 32x128
+    ((128, 256, 1024), (32, 128)),     # the reference's small preset's second GEMM: 8 tiles
+    ((1, 4096, 1024), (32, 128)),      # one row
+    ((64, 512, 2048), (32, 128)),
+])
+def test_lockstep_tile_choice_minimises_rows_per_cu(shape, tile):
+    """Below one round of 256-wide tiles the lock-step tile with the fewest A
+    and W rows per CU (ceil(tiles / 256) x (BM + BN)), the larger on a tie."""
+    lib = _abi.load_library()
+    cfg = (ctypes.c_int32 * 4)()
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(*shape)), cfg) == 0
+    assert (cfg[0], cfg[1]) == tile and cfg[2] == 4
+    assert 2 * cfg[3] <= 160 * 1024
 
 
 def test_force_variant_pins_and_releases():
@@ -113,6 +131,9 @@ def test_force_variant_pins_and_releases():
         _abi.force_variant("deep3")
         assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
         assert tuple(cfg[:3]) == (256, 256, 4)
+        _abi.force_variant("narrow32")
+        assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(16384, 4096, 1024)), cfg) == 0
+        assert tuple(cfg[:3]) == (32, 128, 4)
         with pytest.raises(ValueError):
             _abi.force_variant("huge")
     finally:
