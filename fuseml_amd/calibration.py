@@ -15,8 +15,9 @@ For each group below, on one GPU, the same inputs run three ways:
 Each time is the median of HIP-event timed calls (per call: event, launch,
 event), the best of two alternating passes.  The groups are the benchmark
 configs' six GEMM groups at full size, a K sweep of one- and four-pass chains
-at 256+ tiles, and a few-tile sweep (fewer 128x128 output tiles than CUs) of a
-bias+GELU chain over K.  They replace the reference's NVIDIA tables
+at 256+ tiles, a few-tile sweep (fewer 128x128 output tiles than CUs) of a
+bias+GELU chain over K, and the few-tile groups of the reference's `small` and
+`medium` presets.  They replace the reference's NVIDIA tables
 (fuseml/passes/topology.py:286-571), which on ROCm fall to defaults.
 
 Each row records the chain's elementwise passes
@@ -66,7 +67,13 @@ FEW_TILES: List[Tuple[str, str, int, int, int]] = [
     for (m, n) in ((1024, 1024), (256, 4096), (512, 4096), (2048, 2048))
     for k in (1024, 2048, 4096, 8192)
 ]
-GROUPS = CONFIG_GROUPS + K_SWEEP + FEW_TILES
+# The reference presets' few-tile groups: `medium`'s second GEMM and `small`'s two.
+PRESET_GROUPS: List[Tuple[str, str, int, int, int]] = [
+    ("medium G2", "bias_residual", 2048, 1024, 4096),
+    ("small G1", "bias_gelu", 128, 1024, 256),
+    ("small G2", "bias_residual", 128, 256, 1024),
+]
+GROUPS = CONFIG_GROUPS + K_SWEEP + FEW_TILES + PRESET_GROUPS
 
 # (M, D, I) MLP blocks (linear2(gelu(linear1(x))) + x) for the single-kernel
 # MLP's rule (``--mlp``): the reference's memory-bound widths over M, and C2.
@@ -143,7 +150,7 @@ def _median_ms(fn: Callable[[], object], iters: int) -> float:
 
 
 def measure(groups=GROUPS, passes: int = 2, dev: str = "cuda") -> List[Dict[str, object]]:
-    from .compiler import LONG_K, MIN_TILES_LONG_K, epilogue_passes, fused_beats_eager
+    from .compiler import epilogue_passes, few_tile_verdict, fused_beats_eager
     from .launcher import HipKernelLauncher
 
     rows = []
@@ -163,7 +170,7 @@ def measure(groups=GROUPS, passes: int = 2, dev: str = "cuda") -> List[Dict[str,
         tiles = -(-M // 128) * -(-N // 128)
         addmm = chain != "relu_3red"  # the other chains' GEMM is an addmm (bias in hipBLASLt's epilogue)
         p = epilogue_passes(spec, gemm_is_addmm=addmm)
-        few = K >= LONG_K and tiles < MIN_TILES_LONG_K
+        few = few_tile_verdict(M, N, K) is not None
         rule = (not few) and fused_beats_eager(spec, K, dtype=BF, gemm_is_addmm=addmm)[0]
         rows.append({"group": label, "chain": chain, "M": M, "N": N, "K": K, "passes": p, "tiles_128": tiles,
                      "fused_ms": round(best["fused"], 4), "eager_ms": round(best["eager"], 4),

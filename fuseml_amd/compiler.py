@@ -62,8 +62,17 @@ logger = logging.getLogger("fuseml_amd")
 # min_output_elements=REFERENCE_MIN_OUTPUT_ELEMENTS restores the reference's rule.
 REFERENCE_MIN_OUTPUT_ELEMENTS = 500_000
 MIN_FUSION_OUTPUT_ELEMENTS = 0
-LONG_K = 2048
-MIN_TILES_LONG_K = 512  # 128x128 output tiles: two per CU of MI355X's 256
+# Few-tile groups (fewer 128x128 output tiles than MIN_TILES_LONG_K, two per CU
+# of MI355X's 256) run on one of the library's lock-step tiles (LOCKSTEP_TILES,
+# the choice mirrored by lockstep_tile), whose K loop is bound by the rate at
+# which each CU pulls its tiles' A and W rows through the LDS DMA: such a group
+# fuses while K x (rows per CU) <= MAX_K_ROWS_PER_CU, measured on MI355X
+# (profiles/cost_model_calibration.json: fused 0.66-0.81 of eager's time at
+# 328-393k, 1.00-1.10 at 524-786k).
+MIN_TILES_LONG_K = 512
+MAX_K_ROWS_PER_CU = 448 * 1024
+MI355X_CUS = 256
+LOCKSTEP_TILES = ((128, 128), (64, 128), (32, 128))
 # Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the
 # eager path would run over the [M,N] output) - K_CROSSOVER_OFFSET: the
 # crossover measured on MI355X (fuseml_amd/calibration.py; the measurement is
@@ -161,6 +170,35 @@ def _gemm_k(group: Any) -> Tuple[Optional[int], Any]:
         return None, None
 
 
+def lockstep_tile(M: int, N: int, cus: int = MI355X_CUS) -> Tuple[Tuple[int, int], int]:
+    """The lock-step tile (BM, BN) the library runs an M x N output on below one
+    round of 256-wide tiles, and the A and W rows its busiest CU fetches per
+    unit of K: the fewest ceil(tiles / cus) x (BM + BN), the larger tile on a
+    tie (choose_lockstep in csrc/gemm_epilogue.hip)."""
+    best: Optional[Tuple[Tuple[int, int], int]] = None
+    for bm, bn in LOCKSTEP_TILES:
+        tiles = -(-M // bm) * -(-N // bn)
+        rows = -(-tiles // cus) * (bm + bn)
+        if best is None or rows < best[1]:
+            best = ((bm, bn), rows)
+    assert best is not None
+    return best
+
+
+def few_tile_verdict(M: int, N: int, k_loop: int, min_tiles: int = MIN_TILES_LONG_K) -> Optional[str]:
+    """Why a few-tile group stays eager (None: no objection): fewer than
+    ``min_tiles`` 128x128 output tiles and a K loop of ``k_loop`` over more
+    than MAX_K_ROWS_PER_CU operand rows per CU."""
+    tiles = -(-M // 128) * -(-N // 128)
+    if tiles >= min_tiles:
+        return None
+    (bm, bn), rows = lockstep_tile(M, N)
+    if k_loop * rows <= MAX_K_ROWS_PER_CU:
+        return None
+    return (f"{tiles} output tiles at a K loop of {k_loop}: {rows} operand rows per CU on {bm}x{bn} tiles, "
+            f"K x rows {k_loop * rows} > {MAX_K_ROWS_PER_CU}")
+
+
 def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,
                        min_tiles_long_k: int = MIN_TILES_LONG_K) -> Tuple[bool, str]:
     """Cost model for one addmm/mm trigger: (fuse?, reason)."""
@@ -181,11 +219,9 @@ def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSIO
         return False, f"tiny output {M}x{N}"
     if K % 8 != 0 and m1.dtype != torch.float32:  # the fp32 split pads K
         return False, f"K={K} is not a multiple of 8"
-    tiles = -(-M // 128) * -(-N // 128)
-    k_loop = effective_k(K, m1.dtype)
-    if k_loop >= LONG_K and tiles < min_tiles_long_k:
-        k_txt = f"K={K}" if k_loop == K else f"K={K} (a K loop of {k_loop})"
-        return False, f"{tiles} output tiles at {k_txt}: fewer than two tiles per CU with a long K loop"
+    why = few_tile_verdict(M, N, effective_k(K, m1.dtype), min_tiles_long_k)
+    if why is not None:
+        return False, f"K={K}, " + why
     return True, "fused"
 
 

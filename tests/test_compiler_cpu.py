@@ -189,8 +189,9 @@ def test_cost_model_rules():
 
 
 def test_cost_model_few_tiles_long_k():
-    """K >= 2048 with fewer 128x128 output tiles than two per CU stays eager;
-    two full rounds of tiles, or a short K loop, is fused."""
+    """Fewer 128x128 output tiles than two per CU: fused while K x (operand rows
+    per CU on the library's lock-step tile) stays within the measured budget;
+    two full rounds of tiles are fused whatever K."""
     from torch.fx.experimental.proxy_tensor import make_fx
 
     def f(x, w):
@@ -200,13 +201,37 @@ def test_cost_model_few_tiles_long_k():
         gm = make_fx(f)(torch.randn(M, K, dtype=BF), torch.randn(K, N, dtype=BF))
         return [n for n in gm.graph.nodes if n.op == "call_function"][0]
 
-    ok, why = trigger_is_fusible(node(1024, 2048, 1024))      # 8 x 8 = 64 tiles
-    assert ok is False and "64 output tiles at K=2048" in why
-    assert trigger_is_fusible(node(1024, 2048, 1024), min_tiles_long_k=0)[0]
-    assert not trigger_is_fusible(node(2048, 2048, 2048))[0]   # 16 x 16 = 256 tiles
+    # 8 x 8 = 64 tiles: 256 of 32x128, 160 rows per CU
+    ok, why = trigger_is_fusible(node(1024, 4096, 1024))
+    assert ok is False and "64 output tiles at a K loop of 4096" in why and "32x128" in why
+    assert trigger_is_fusible(node(1024, 4096, 1024), min_tiles_long_k=0)[0]
+    assert trigger_is_fusible(node(1024, 2048, 1024))[0]       # 160 x 2048 rows within the budget
+    assert not trigger_is_fusible(node(2048, 2048, 2048))[0]   # 256 tiles of 128x128: 256 x 2048 rows
+    assert trigger_is_fusible(node(2048, 1024, 2048))[0]       # 256 x 1024
     assert trigger_is_fusible(node(4096, 2048, 2048))[0]       # 32 x 16 = 512 tiles
-    assert trigger_is_fusible(node(1024, 2040, 1024))[0]       # K < 2048
     assert trigger_is_fusible(node(1024, 1024, 1024))[0]
+    # the reference's medium preset's second GEMM (128 tiles, 64x128 tiles, K = 4096) stays eager
+    assert not trigger_is_fusible(node(2048, 4096, 1024))[0]
+
+
+def test_lockstep_tile_mirrors_the_library():
+    """compiler.lockstep_tile names the tile the library's own choice picks
+    (fuseml_gemm_epilogue_config, 256 CUs without a device)."""
+    import ctypes
+
+    from fuseml_amd import _abi
+
+    lib = _abi.load_library()
+    cfg = (ctypes.c_int32 * 4)()
+    for M, N in ((1, 4096), (64, 512), (128, 256), (128, 1024), (512, 4096), (1000, 900), (1024, 1024),
+                 (2048, 1024), (2048, 2048), (2048, 4096)):
+        d = _abi.GemmDesc()
+        d.M, d.N, d.K = M, N, 1024
+        d.a, d.lda, d.b, d.ldb = 0x10000, 1024, 0x20000, 1024
+        d.ab_dtype = _abi.BF16
+        d.out.ptr, d.out.ld, d.out.dtype = 0x30000, N, _abi.BF16
+        assert lib.fuseml_gemm_epilogue_config(ctypes.byref(d), cfg) == 0, _abi.last_error(lib)
+        assert (cfg[0], cfg[1]) == comp.lockstep_tile(M, N)[0], (M, N)
 
 
 class _TwoReductionChains(nn.Module):

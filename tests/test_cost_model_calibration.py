@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from fuseml_amd import calibration as cal
-from fuseml_amd.compiler import LONG_K, MIN_TILES_LONG_K, epilogue_passes, fused_beats_eager
+from fuseml_amd.compiler import MIN_TILES_LONG_K, epilogue_passes, few_tile_verdict, fused_beats_eager
 from fuseml_amd.mlp import mlp_block_beats_two_launches
 
 PROFILES = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "profiles")
@@ -31,6 +31,9 @@ MLP_PATH = os.path.join(PROFILES, "mlp_block_crossover.json")
 # up a few per cent (bias + residual at K = 2048: fused 3.4% faster, sent to
 # eager; a 2048x2048 bias + GELU at the same K: fused 4.6% slower).
 TIE = 0.04
+# The MLP crossover's near-ties move further between boxes: M = 16384, D = 512
+# measured single/two 1.06 on one box and 0.94-0.96 in three runs on another.
+MLP_TIE = 0.07
 
 
 def _rows():
@@ -41,8 +44,7 @@ def _rows():
 def _decision(row):
     spec, _ = cal._spec(row["chain"])
     addmm = row["chain"] != "relu_3red"
-    tiles = -(-row["M"] // 128) * -(-row["N"] // 128)
-    if row["K"] >= LONG_K and tiles < MIN_TILES_LONG_K:
+    if few_tile_verdict(row["M"], row["N"], row["K"]) is not None:
         return False
     return fused_beats_eager(spec, row["K"], dtype=torch.bfloat16, gemm_is_addmm=addmm)[0]
 
@@ -51,7 +53,10 @@ def test_calibration_covers_the_config_groups_and_both_rules():
     rows = _rows()
     labels = {r["group"] for r in rows}
     assert {g[0] for g in cal.CONFIG_GROUPS} <= labels
-    assert any(r["tiles_128"] < MIN_TILES_LONG_K for r in rows)          # the few-tile rule is exercised
+    few = [r for r in rows if r["tiles_128"] < MIN_TILES_LONG_K]
+    # the few-tile rule is exercised on both sides
+    assert any(few_tile_verdict(r["M"], r["N"], r["K"]) is None for r in few)
+    assert any(few_tile_verdict(r["M"], r["N"], r["K"]) is not None for r in few)
     assert {1, 2, 4} <= {r["passes"] for r in rows}                       # several pass counts
     for r in rows:
         spec, _ = cal._spec(r["chain"])
@@ -74,14 +79,14 @@ def _mlp_rows():
 
 def test_mlp_crossover_covers_both_outcomes():
     rows = _mlp_rows()
-    assert any(r["single_over_two"] < 1 - TIE for r in rows) and any(r["single_over_two"] > 1 + TIE for r in rows)
+    assert any(r["single_over_two"] < 1 - MLP_TIE for r in rows) and any(r["single_over_two"] > 1 + MLP_TIE for r in rows)
     assert {256, 512, 1024} <= {r["D"] for r in rows}
 
 
 @pytest.mark.parametrize("row", _mlp_rows(), ids=lambda r: f"M{r['M']}-D{r['D']}-I{r['I']}")
 def test_mlp_rule_picks_the_measured_winner(row):
     ratio = row["single_over_two"]
-    if abs(ratio - 1.0) < TIE:
+    if abs(ratio - 1.0) < MLP_TIE:
         pytest.skip(f"tie: single/two = {ratio:.3f}")
     binds = mlp_block_beats_two_launches(row["M"], row["D"], row["I"])[0]
     assert binds == (ratio < 1.0), f"{row}: rule binds={binds}"

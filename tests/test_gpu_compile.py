@@ -47,24 +47,30 @@ def _close(got, ref, what):
 
 
 def test_few_tiles_long_k_is_routed_to_eager():
-    """Cost model on the device: Linear(2048 -> 1024) + GELU at M=1024 has 64
-    output tiles of 128x128 at K=2048, so the group runs eager; lowering the
-    tile floor fuses the same module, and both match eager."""
+    """Cost model on the device: Linear(4096 -> 1024) + GELU at M=1024 has 64
+    output tiles of 128x128 (256 of the 32x128 tiles it would run on, 160
+    operand rows per CU) at K=4096, over the rows x K budget, so the group runs
+    eager; with the few-tile rule off (min_tiles_long_k=0) the same module is
+    fused, and both match eager.  At K=2048 the default fuses it."""
+    from fuseml_amd.compiler import MIN_TILES_LONG_K
+
     gen = torch.Generator().manual_seed(3)
-    lin = torch.nn.Linear(2048, 1024).to(torch.bfloat16)
-    m = torch.nn.Sequential(lin, torch.nn.GELU()).to("cuda")
-    x = torch.randn(1024, 2048, generator=gen).to(torch.bfloat16).to("cuda")
-    with torch.no_grad():
-        ref = m(x)
-        compiled, be = _compile(m, min_tiles_long_k=256)
-        out = compiled(x)
-    assert be.launchers == [] and be.fusion_applied is False
-    _close(out, _f64(ref), "eager-routed Linear+GELU")
-    with torch.no_grad():
-        compiled, be = _compile(m)
-        out = compiled(x)
-    assert be.fusion_applied and _launches(be) == 1
-    _close(out, _f64(ref), "fused Linear+GELU")
+    for K, fused_by_default in ((4096, False), (2048, True)):
+        lin = torch.nn.Linear(K, 1024).to(torch.bfloat16)
+        m = torch.nn.Sequential(lin, torch.nn.GELU()).to("cuda")
+        x = torch.randn(1024, K, generator=gen).to(torch.bfloat16).to("cuda")
+        print(f"case few-tile Linear({K} -> 1024) + GELU at M=1024", flush=True)
+        with torch.no_grad():
+            ref = m(x)
+            compiled, be = _compile(m, min_tiles_long_k=MIN_TILES_LONG_K)
+            out = compiled(x)
+        assert bool(be.launchers) == fused_by_default and be.fusion_applied == fused_by_default
+        _close(out, _f64(ref), f"default-routed Linear({K})+GELU")
+        with torch.no_grad():
+            compiled, be = _compile(m)
+            out = compiled(x)
+        assert be.fusion_applied and _launches(be) == 1
+        _close(out, _f64(ref), f"fused Linear({K})+GELU")
 
 
 class _NegReluAmax(torch.nn.Module):
