@@ -67,9 +67,11 @@ FEW_TILES: List[Tuple[str, str, int, int, int]] = [
     for (m, n) in ((1024, 1024), (256, 4096), (512, 4096), (2048, 2048))
     for k in (1024, 2048, 4096, 8192)
 ]
-# The reference presets' few-tile groups: `medium`'s second GEMM and `small`'s two.
+# The reference presets' few-tile groups: `medium`'s and `stacked_memory_bound`'s
+# second GEMMs and `small`'s two.
 PRESET_GROUPS: List[Tuple[str, str, int, int, int]] = [
     ("medium G2", "bias_residual", 2048, 1024, 4096),
+    ("stacked_memory_bound G2", "bias_residual", 8192, 512, 2048),
     ("small G1", "bias_gelu", 128, 1024, 256),
     ("small G2", "bias_residual", 128, 256, 1024),
 ]

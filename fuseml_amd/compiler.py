@@ -66,11 +66,12 @@ MIN_FUSION_OUTPUT_ELEMENTS = 0
 # of MI355X's 256) run on one of the library's lock-step tiles (LOCKSTEP_TILES,
 # the choice mirrored by lockstep_tile), whose K loop is bound by the rate at
 # which each CU pulls its tiles' A and W rows through the LDS DMA: such a group
-# fuses while K x (rows per CU) <= MAX_K_ROWS_PER_CU, measured on MI355X
-# (profiles/cost_model_calibration.json: fused 0.66-0.81 of eager's time at
-# 328-393k, 1.00-1.10 at 524-786k).
+# fuses while K x (rows per CU, weighted as lockstep_tile weighs them) <=
+# MAX_K_ROWS_PER_CU, measured on MI355X (profiles/cost_model_calibration.json:
+# fused 0.36-0.77 of eager's time up to 614k, 0.95-1.01 at 768k-1229k, 1.06-1.33
+# beyond or with a residual read at 768k).
 MIN_TILES_LONG_K = 512
-MAX_K_ROWS_PER_CU = 448 * 1024
+MAX_K_ROWS_PER_CU = 704 * 1024
 MI355X_CUS = 256
 LOCKSTEP_TILES = ((128, 128), (64, 128), (32, 128))
 # Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the
@@ -170,19 +171,20 @@ def _gemm_k(group: Any) -> Tuple[Optional[int], Any]:
         return None, None
 
 
-def lockstep_tile(M: int, N: int, cus: int = MI355X_CUS) -> Tuple[Tuple[int, int], int]:
+def lockstep_tile(M: int, N: int, cus: int = MI355X_CUS) -> Tuple[Tuple[int, int], float]:
     """The lock-step tile (BM, BN) the library runs an M x N output on below one
-    round of 256-wide tiles, and the A and W rows its busiest CU fetches per
-    unit of K: the fewest ceil(tiles / cus) x (BM + BN), the larger tile on a
-    tie (choose_lockstep in csrc/gemm_epilogue.hip)."""
+    round of 256-wide tiles, and its busiest CU's K-loop work in operand rows
+    per unit of K: ceil(tiles / cus) x (BM + BN), x 1.6 when every CU holds at
+    most one workgroup (one wave per SIMD); the least, the larger tile on a tie
+    (choose_lockstep in csrc/gemm_epilogue.hip)."""
     best: Optional[Tuple[Tuple[int, int], int]] = None
     for bm, bn in LOCKSTEP_TILES:
         tiles = -(-M // bm) * -(-N // bn)
-        rows = -(-tiles // cus) * (bm + bn)
-        if best is None or rows < best[1]:
-            best = ((bm, bn), rows)
+        work = -(-tiles // cus) * (bm + bn) * (8 if tiles <= cus else 5)
+        if best is None or work < best[1]:
+            best = ((bm, bn), work)
     assert best is not None
-    return best
+    return best[0], best[1] / 5
 
 
 def few_tile_verdict(M: int, N: int, k_loop: int, min_tiles: int = MIN_TILES_LONG_K) -> Optional[str]:
@@ -195,8 +197,8 @@ def few_tile_verdict(M: int, N: int, k_loop: int, min_tiles: int = MIN_TILES_LON
     (bm, bn), rows = lockstep_tile(M, N)
     if k_loop * rows <= MAX_K_ROWS_PER_CU:
         return None
-    return (f"{tiles} output tiles at a K loop of {k_loop}: {rows} operand rows per CU on {bm}x{bn} tiles, "
-            f"K x rows {k_loop * rows} > {MAX_K_ROWS_PER_CU}")
+    return (f"{tiles} output tiles at a K loop of {k_loop}: {rows:g} operand rows per CU on {bm}x{bn} tiles, "
+            f"K x rows {k_loop * rows:.0f} > {MAX_K_ROWS_PER_CU}")
 
 
 def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSION_OUTPUT_ELEMENTS,

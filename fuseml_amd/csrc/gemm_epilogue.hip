@@ -89,22 +89,24 @@ int forced_variant() {
 int match_fixed_chain(const fuseml_gemm_desc& d);
 
 // Below one round of 256-wide tiles, one of the lock-step variants (128x128,
-// 64x128, 32x128): the one whose busiest CU fetches the fewest operand bytes
-// per unit of K, ceil(tiles / CUs) x (BM + BN) rows, the larger tile on a tie.
-// Each CU moves its tiles' A and W rows through the LDS DMA at a roughly fixed
-// rate (37-48 GB/s measured, whatever the tile), so below two 128x128 tiles
-// per CU a narrower tile spreads the same K over more CUs.  Measured (bias +
-// GELU or bias + residual, M x N x K): 128x1024x256 9.6 -> 5.9 us and
-// 1024x1024x1024 16.8 -> 9.9 us on 32x128 tiles; 2048x1024x4096 44 -> 31 us
-// on 64x128 tiles (32x128 tiles, two per CU there, take 35); 2048x4096x1024
-// stays on 128x128 tiles (30.6 us; 64x128 33, 32x128 44).
+// 64x128, 32x128): the one whose busiest CU has the least K-loop work,
+// ceil(tiles / CUs) x (BM + BN) operand rows per unit of K, weighted 8:5 when
+// every CU holds at most one workgroup (one wave per SIMD hides less of the
+// LDS DMA's latency than two), the larger tile on a tie.  Each CU moves its
+// tiles' A and W rows through the LDS DMA at a roughly fixed rate (37-48 GB/s
+// measured, whatever the tile), so below two 128x128 tiles per CU a narrower
+// tile spreads the same K over more CUs or more waves.  Measured (bias + GELU
+// or bias + residual, M x N x K, us): 128x1024x256 9.6 -> 5.9 and
+// 1024x1024x1024 16.8 -> 9.9 on 32x128 tiles; 2048x1024x4096 44.7 -> 31.7,
+// 2048x2048x1024 20.0 -> 17.7 and 8192x512x2048 31.5 -> 28.8 on 64x128 tiles;
+// 2048x4096x1024 stays on 128x128 tiles (32.6; 64x128 33.8, 32x128 44).
 TileConfig choose_lockstep(const fuseml_gemm_desc& d, int cus) {
   const TileConfig* cand[3] = {&kSmall, &kNarrow64, &kNarrow32};
   const TileConfig* best = cand[0];
   int64_t best_rows = 0;
   for (const TileConfig* c : cand) {
     const int64_t tiles = cdiv(d.M, c->bm) * cdiv(d.N, c->bn);
-    const int64_t rows = cdiv(tiles, cus) * (c->bm + c->bn);
+    const int64_t rows = cdiv(tiles, cus) * (c->bm + c->bn) * (tiles <= cus ? 8 : 5);
     if (c == cand[0] || rows < best_rows) {
       best = c;
       best_rows = rows;

@@ -109,11 +109,14 @@ def test_tile_config_choice():
     ((1024, 1024, 1024), (32, 128)),   # 64 tiles of 128x128: 256 of 32x128
     ((128, 256, 1024), (32, 128)),     # the reference's small preset's second GEMM: 8 tiles
     ((1, 4096, 1024), (32, 128)),      # one row
+    ((2048, 2048, 1024), (64, 128)),   # 256 tiles of 128x128 (one per CU) against 512 of 64x128 (two)
+    ((8192, 512, 2048), (64, 128)),
     ((64, 512, 2048), (32, 128)),
 ])
 def test_lockstep_tile_choice_minimises_rows_per_cu(shape, tile):
-    """Below one round of 256-wide tiles the lock-step tile with the fewest A
-    and W rows per CU (ceil(tiles / 256) x (BM + BN)), the larger on a tie."""
+    """Below one round of 256-wide tiles the lock-step tile with the least
+    K-loop work per CU: ceil(tiles / 256) x (BM + BN) operand rows, weighted
+    8:5 when no CU holds two workgroups, the larger tile on a tie."""
     lib = _abi.load_library()
     cfg = (ctypes.c_int32 * 4)()
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(*shape)), cfg) == 0

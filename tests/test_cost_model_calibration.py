@@ -31,6 +31,10 @@ MLP_PATH = os.path.join(PROFILES, "mlp_block_crossover.json")
 # up a few per cent (bias + residual at K = 2048: fused 3.4% faster, sent to
 # eager; a 2048x2048 bias + GELU at the same K: fused 4.6% slower).
 TIE = 0.04
+# Few-tile groups take 10-50 us, where eager's time per call sits on its host
+# floor, which moves between boxes (1024x1024 at K = 4096: eager 24.1 us on one
+# box, 26.8 on another, fused 25.4-25.8 on both): within 8% they are ties.
+FEW_TILE_TIE = 0.08
 # The MLP crossover's near-ties move further between boxes: M = 16384, D = 512
 # measured single/two 1.06 on one box and 0.94-0.96 in three runs on another.
 MLP_TIE = 0.07
@@ -66,7 +70,7 @@ def test_calibration_covers_the_config_groups_and_both_rules():
 @pytest.mark.parametrize("row", _rows(), ids=lambda r: r["group"])
 def test_rule_picks_the_measured_winner(row):
     ratio = row["fused_ms"] / row["eager_ms"]
-    if abs(ratio - 1.0) < TIE:
+    if abs(ratio - 1.0) < (FEW_TILE_TIE if row["tiles_128"] < MIN_TILES_LONG_K else TIE):
         pytest.skip(f"tie: fused/eager = {ratio:.3f}")
     assert _decision(row) == (ratio < 1.0), (
         f"{row['group']}: fused {row['fused_ms']} ms, eager {row['eager_ms']} ms, rule fuses={_decision(row)}")
