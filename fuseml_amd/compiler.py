@@ -63,17 +63,20 @@ logger = logging.getLogger("fuseml_amd")
 REFERENCE_MIN_OUTPUT_ELEMENTS = 500_000
 MIN_FUSION_OUTPUT_ELEMENTS = 0
 # Few-tile groups (fewer 128x128 output tiles than MIN_TILES_LONG_K, two per CU
-# of MI355X's 256) run on one of the library's lock-step tiles (LOCKSTEP_TILES,
-# the choice mirrored by lockstep_tile), whose K loop is bound by the rate at
+# of MI355X's 256) run on one of the library's smaller tiles (PARTIAL_ROUND_TILES,
+# the choice mirrored by partial_round_tile), whose K loop is bound by the rate at
 # which each CU pulls its tiles' A and W rows through the LDS DMA: such a group
-# fuses while K x (rows per CU, weighted as lockstep_tile weighs them) <=
+# fuses while K x (rows per CU, weighted as partial_round_tile weighs them) <=
 # MAX_K_ROWS_PER_CU, measured on MI355X (profiles/cost_model_calibration.json:
-# fused 0.36-0.77 of eager's time up to 614k, 0.95-1.01 at 768k-1229k, 1.06-1.33
-# beyond or with a residual read at 768k).
+# fused 0.37-0.80 of eager's time up to 614k, 1.00-1.09 at 768k-1229k, 1.07-1.31
+# beyond).
 MIN_TILES_LONG_K = 512
 MAX_K_ROWS_PER_CU = 704 * 1024
 MI355X_CUS = 256
-LOCKSTEP_TILES = ((128, 128), (64, 128), (32, 128))
+# (BM, BN, weight with at most one workgroup on a CU, with two): the library's
+# tiles below one round of 256x256 tiles (choose_partial_round in
+# csrc/gemm_epilogue.hip): three lock-step tiles and the 256x128 ping-pong one.
+PARTIAL_ROUND_TILES = ((128, 128, 8, 5), (64, 128, 8, 5), (32, 128, 8, 5), (256, 128, 6, 6))
 # Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the
 # eager path would run over the [M,N] output) - K_CROSSOVER_OFFSET: the
 # crossover measured on MI355X (fuseml_amd/calibration.py; the measurement is
@@ -171,16 +174,17 @@ def _gemm_k(group: Any) -> Tuple[Optional[int], Any]:
         return None, None
 
 
-def lockstep_tile(M: int, N: int, cus: int = MI355X_CUS) -> Tuple[Tuple[int, int], float]:
-    """The lock-step tile (BM, BN) the library runs an M x N output on below one
-    round of 256-wide tiles, and its busiest CU's K-loop work in operand rows
-    per unit of K: ceil(tiles / cus) x (BM + BN), x 1.6 when every CU holds at
-    most one workgroup (one wave per SIMD); the least, the larger tile on a tie
-    (choose_lockstep in csrc/gemm_epilogue.hip)."""
+def partial_round_tile(M: int, N: int, cus: int = MI355X_CUS) -> Tuple[Tuple[int, int], float]:
+    """The tile (BM, BN) the library runs an M x N output on below one round of
+    256x256 tiles, and its busiest CU's K-loop work in operand rows per unit of
+    K: ceil(tiles / cus) x (BM + BN), weighted by how fast a CU moves them (x
+    1.6 for a lock-step tile when no CU holds two workgroups, x 1.2 for the
+    ping-pong tile); the least, the first listed on a tie
+    (choose_partial_round in csrc/gemm_epilogue.hip)."""
     best: Optional[Tuple[Tuple[int, int], int]] = None
-    for bm, bn in LOCKSTEP_TILES:
+    for bm, bn, w_one, w_two in PARTIAL_ROUND_TILES:
         tiles = -(-M // bm) * -(-N // bn)
-        work = -(-tiles // cus) * (bm + bn) * (8 if tiles <= cus else 5)
+        work = -(-tiles // cus) * (bm + bn) * (w_one if tiles <= cus else w_two)
         if best is None or work < best[1]:
             best = ((bm, bn), work)
     assert best is not None
@@ -194,7 +198,7 @@ def few_tile_verdict(M: int, N: int, k_loop: int, min_tiles: int = MIN_TILES_LON
     tiles = -(-M // 128) * -(-N // 128)
     if tiles >= min_tiles:
         return None
-    (bm, bn), rows = lockstep_tile(M, N)
+    (bm, bn), rows = partial_round_tile(M, N)
     if k_loop * rows <= MAX_K_ROWS_PER_CU:
         return None
     return (f"{tiles} output tiles at a K loop of {k_loop}: {rows:g} operand rows per CU on {bm}x{bn} tiles, "

@@ -60,11 +60,12 @@ constexpr int64_t kTileSpan = 256;  // largest tile edge of any variant
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Pinned variant: 0 automatic, else 1 + index into {large, deep, deep3, small,
-// deep3-generic, narrow64, narrow32} (deep3-generic: deep3 with the generic op
-// loop even where a fixed chain matches).  Initialised once per process from FUSEML_HIP_TILE, changed
+// deep3-generic, narrow64, narrow32, large128} (deep3-generic: deep3 with the
+// generic op loop even where a fixed chain matches).  Initialised once per process from FUSEML_HIP_TILE, changed
 // only through fuseml_gemm_epilogue_force_variant.
-constexpr const char* kVariantNames[] = {"large", "deep", "deep3", "small", "deep3-generic", "narrow64", "narrow32"};
-constexpr int kNumVariantNames = 7;
+constexpr const char* kVariantNames[] = {"large", "deep", "deep3", "small", "deep3-generic", "narrow64", "narrow32",
+                                         "large128"};
+constexpr int kNumVariantNames = 8;
 constexpr int kForcedDeep3Generic = 5;
 std::atomic<int> g_forced_variant{-1};  // -1: environment not read yet
 
@@ -88,28 +89,35 @@ int forced_variant() {
 
 int match_fixed_chain(const fuseml_gemm_desc& d);
 
-// Below one round of 256-wide tiles, one of the lock-step variants (128x128,
-// 64x128, 32x128): the one whose busiest CU has the least K-loop work,
-// ceil(tiles / CUs) x (BM + BN) operand rows per unit of K, weighted 8:5 when
-// every CU holds at most one workgroup (one wave per SIMD hides less of the
-// LDS DMA's latency than two), the larger tile on a tie.  Each CU moves its
-// tiles' A and W rows through the LDS DMA at a roughly fixed rate (37-48 GB/s
-// measured, whatever the tile), so below two 128x128 tiles per CU a narrower
-// tile spreads the same K over more CUs or more waves.  Measured (bias + GELU
-// or bias + residual, M x N x K, us): 128x1024x256 9.6 -> 5.9 and
+// Below one round of 256x256 tiles: the 128x128, 64x128 or 32x128 lock-step
+// tile (4 waves, two workgroups per CU) or the 256x128 ping-pong tile (8
+// waves, one per CU), whichever gives its busiest CU the least K-loop work:
+// ceil(tiles / CUs) x (BM + BN) operand rows per unit of K, weighted by how
+// fast a CU moves them: 5 for the lock-step tiles with two workgroups on some
+// CU, 8 with at most one (one wave per SIMD hides less of the LDS DMA's
+// latency), 6 for the ping-pong tile; the first of the list on a tie.  Each
+// CU moves its tiles' A and W rows through the LDS DMA at a roughly fixed rate
+// (37-48 GB/s measured, whatever the tile), so below two 128x128 tiles per CU
+// a narrower tile spreads the same K over more CUs or more waves.  Measured
+// (bias + GELU or bias + residual, M x N x K, us): 128x1024x256 9.6 -> 5.9 and
 // 1024x1024x1024 16.8 -> 9.9 on 32x128 tiles; 2048x1024x4096 44.7 -> 31.7,
 // 2048x2048x1024 20.0 -> 17.7 and 8192x512x2048 31.5 -> 28.8 on 64x128 tiles;
-// 2048x4096x1024 stays on 128x128 tiles (32.6; 64x128 33.8, 32x128 44).
-TileConfig choose_lockstep(const fuseml_gemm_desc& d, int cus) {
-  const TileConfig* cand[3] = {&kSmall, &kNarrow64, &kNarrow32};
-  const TileConfig* best = cand[0];
-  int64_t best_rows = 0;
-  for (const TileConfig* c : cand) {
-    const int64_t tiles = cdiv(d.M, c->bm) * cdiv(d.N, c->bn);
-    const int64_t rows = cdiv(tiles, cus) * (c->bm + c->bn) * (tiles <= cus ? 8 : 5);
-    if (c == cand[0] || rows < best_rows) {
-      best = c;
-      best_rows = rows;
+// 2048x4096x1024 33.0 -> 29.0 and 4096x2048x1024 31.8 -> 29.5 on 256x128
+// ping-pong tiles (64x128 tiles there: 35.0 and 33.2).
+TileConfig choose_partial_round(const fuseml_gemm_desc& d, int cus) {
+  struct Cand {
+    const TileConfig* c;
+    int w_one, w_two;  // weight with at most one / with two workgroups on a CU
+  };
+  const Cand cand[4] = {{&kSmall, 8, 5}, {&kNarrow64, 8, 5}, {&kNarrow32, 8, 5}, {&kLarge128, 6, 6}};
+  const TileConfig* best = cand[0].c;
+  int64_t best_work = 0;
+  for (const Cand& k : cand) {
+    const int64_t tiles = cdiv(d.M, k.c->bm) * cdiv(d.N, k.c->bn);
+    const int64_t work = cdiv(tiles, cus) * (k.c->bm + k.c->bn) * (tiles <= cus ? k.w_one : k.w_two);
+    if (k.c == cand[0].c || work < best_work) {
+      best = k.c;
+      best_work = work;
     }
   }
   return *best;
@@ -128,6 +136,7 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
     case kForcedDeep3Generic: return d.K % 64 == 0 ? kDeep3 : kDeep;
     case 6: return kNarrow64;
     case 7: return kNarrow32;
+    case 8: return kLarge128;
     default: break;
   }
   // A 256x256 tile keeps the LDS traffic per MFMA low enough for the MFMA pipe
@@ -142,11 +151,12 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
   // bias+ReLU, GELU(tanh), bias+residual, the act-heavy chain) except
   // bias+GELU(erf), which ties or loses up to 1.5%.  With K % 64 != 0 the
   // two-stage one takes over from K = 8192.
-  // The 128x128 variant while its tiles fit one round at two workgroups per
-  // CU (4 x large_tiles <= 2 x cus): at 128 large tiles on 256 CUs it is 7-17%
-  // faster (bias+GELU at K = 512-1024), from 144 on the 256-wide one is.
+  // Below one round of 256x256 tiles (2 x large_tiles <= cus) the smaller
+  // tiles (choose_partial_round): at 128 large tiles on 256 CUs the 128x128
+  // one was 7-17% faster than 256x256 (bias+GELU at K = 512-1024), from 144
+  // on the 256x256 ones are.
   const int64_t large_tiles = cdiv(d.M, 256) * cdiv(d.N, 256);
-  if (2 * large_tiles <= cus) return choose_lockstep(d, cus);
+  if (2 * large_tiles <= cus) return choose_partial_round(d, cus);
   if (d.K % 64 == 0 && (d.K >= 8192 || (d.K >= 2048 && large_tiles >= cus))) return kDeep3;
   if (d.K % 64 == 0 && d.K >= 1024 && large_tiles >= cus) {
     const int ch = match_fixed_chain(d);
@@ -520,7 +530,8 @@ int fuseml_gemm_epilogue_force_variant(const char* name) {
   g_last_error[0] = '\0';
   const int v = variant_code(name);
   if (v < 0) {
-    set_error("unknown variant '%s' (large, deep, deep3, small, deep3-generic, narrow64, narrow32 or auto)", name);
+    set_error("unknown variant '%s' (large, deep, deep3, small, deep3-generic, narrow64, narrow32, large128 or auto)",
+              name);
     return FUSEML_EINVAL;
   }
   forced_variant();  // the environment is read first, so it cannot override this later
@@ -581,6 +592,8 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
     e = launch_fixed<kDeep3>(d, ch, stream, cus);
   else if (c.sched == kDeep.sched)
     e = launch_variant<kDeep>(d, stream, cus);
+  else if (c.sched == kLarge.sched && c.bn == kLarge128.bn)
+    e = launch_variant<kLarge128>(d, stream, cus);
   else if (c.sched == kLarge.sched)
     e = launch_variant<kLarge>(d, stream, cus);
   else if (c.sched == kDeep3.sched)

@@ -214,8 +214,8 @@ def test_cost_model_few_tiles_long_k():
     assert not trigger_is_fusible(node(2048, 4096, 1024))[0]
 
 
-def test_lockstep_tile_mirrors_the_library():
-    """compiler.lockstep_tile names the tile the library's own choice picks
+def test_partial_round_tile_mirrors_the_library():
+    """compiler.partial_round_tile names the tile the library's own choice picks
     (fuseml_gemm_epilogue_config, 256 CUs without a device)."""
     import ctypes
 
@@ -231,7 +231,7 @@ def test_lockstep_tile_mirrors_the_library():
         d.ab_dtype = _abi.BF16
         d.out.ptr, d.out.ld, d.out.dtype = 0x30000, N, _abi.BF16
         assert lib.fuseml_gemm_epilogue_config(ctypes.byref(d), cfg) == 0, _abi.last_error(lib)
-        assert (cfg[0], cfg[1]) == comp.lockstep_tile(M, N)[0], (M, N)
+        assert (cfg[0], cfg[1]) == comp.partial_round_tile(M, N)[0], (M, N)
 
 
 class _TwoReductionChains(nn.Module):

@@ -168,7 +168,7 @@ def test_reductions_parity(axis, shape):
 # schedules on every chain, on ragged edges and on K that ends mid-stage.
 # ---------------------------------------------------------------------------
 
-VARIANTS = ["large", "deep", "deep3", "deep3-generic", "small", "narrow64", "narrow32"]
+VARIANTS = ["large", "deep", "deep3", "deep3-generic", "small", "narrow64", "narrow32", "large128"]
 
 
 def _k_for(variant, K):
