@@ -73,10 +73,10 @@ MIN_FUSION_OUTPUT_ELEMENTS = 0
 MIN_TILES_LONG_K = 512
 MAX_K_ROWS_PER_CU = 704 * 1024
 MI355X_CUS = 256
-# (BM, BN, weight with at most one workgroup on a CU, with two): the library's
-# tiles below one round of 256x256 tiles (choose_partial_round in
-# csrc/gemm_epilogue.hip): three lock-step tiles and the 256x128 ping-pong one.
-PARTIAL_ROUND_TILES = ((128, 128, 8, 5), (64, 128, 8, 5), (32, 128, 8, 5), (256, 128, 6, 6))
+# (BM, BN, lock-step?): the library's tiles below one round of 256x256 tiles
+# (choose_partial_round in csrc/gemm_epilogue.hip): three lock-step tiles and
+# the 256x128 ping-pong one.
+PARTIAL_ROUND_TILES = ((128, 128, True), (64, 128, True), (32, 128, True), (256, 128, False))
 # Fuse a group only while K <= K_PER_EPILOGUE_PASS * (elementwise passes the
 # eager path would run over the [M,N] output) - K_CROSSOVER_OFFSET: the
 # crossover measured on MI355X (fuseml_amd/calibration.py; the measurement is
@@ -174,17 +174,19 @@ def _gemm_k(group: Any) -> Tuple[Optional[int], Any]:
         return None, None
 
 
-def partial_round_tile(M: int, N: int, cus: int = MI355X_CUS) -> Tuple[Tuple[int, int], float]:
-    """The tile (BM, BN) the library runs an M x N output on below one round of
-    256x256 tiles, and its busiest CU's K-loop work in operand rows per unit of
-    K: ceil(tiles / cus) x (BM + BN), weighted by how fast a CU moves them (x
-    1.6 for a lock-step tile when no CU holds two workgroups, x 1.2 for the
-    ping-pong tile); the least, the first listed on a tie
+def partial_round_tile(M: int, N: int, K: int, cus: int = MI355X_CUS) -> Tuple[Tuple[int, int], float]:
+    """The tile (BM, BN) the library runs an M x N x K GEMM on below one round
+    of 256x256 tiles, and its busiest CU's K-loop work in operand rows per
+    unit of K: ceil(tiles / cus) x (BM + BN), weighted by how fast a CU moves
+    them (a lock-step tile x 1.6 when no CU holds two workgroups, x 1.4 for K >
+    2048; the ping-pong tile x 1.2); the least, the first listed on a tie
     (choose_partial_round in csrc/gemm_epilogue.hip)."""
+    one = 7 if K > 2048 else 8
     best: Optional[Tuple[Tuple[int, int], int]] = None
-    for bm, bn, w_one, w_two in PARTIAL_ROUND_TILES:
+    for bm, bn, lockstep in PARTIAL_ROUND_TILES:
         tiles = -(-M // bm) * -(-N // bn)
-        work = -(-tiles // cus) * (bm + bn) * (w_one if tiles <= cus else w_two)
+        weight = (one if tiles <= cus else 5) if lockstep else 6
+        work = -(-tiles // cus) * (bm + bn) * weight
         if best is None or work < best[1]:
             best = ((bm, bn), work)
     assert best is not None
@@ -198,7 +200,7 @@ def few_tile_verdict(M: int, N: int, k_loop: int, min_tiles: int = MIN_TILES_LON
     tiles = -(-M // 128) * -(-N // 128)
     if tiles >= min_tiles:
         return None
-    (bm, bn), rows = partial_round_tile(M, N)
+    (bm, bn), rows = partial_round_tile(M, N, k_loop)
     if k_loop * rows <= MAX_K_ROWS_PER_CU:
         return None
     return (f"{tiles} output tiles at a K loop of {k_loop}: {rows:g} operand rows per CU on {bm}x{bn} tiles, "

@@ -95,7 +95,9 @@ int match_fixed_chain(const fuseml_gemm_desc& d);
 // ceil(tiles / CUs) x (BM + BN) operand rows per unit of K, weighted by how
 // fast a CU moves them: 5 for the lock-step tiles with two workgroups on some
 // CU, 8 with at most one (one wave per SIMD hides less of the LDS DMA's
-// latency), 6 for the ping-pong tile; the first of the list on a tie.  Each
+// latency and none of the epilogue; 7 for K > 2048), 6 for the ping-pong
+// tile; the first of the list on a tie.  Also for M <= 128 at any N, where a
+// 256-row tile is at least half padding.  Each
 // CU moves its tiles' A and W rows through the LDS DMA at a roughly fixed rate
 // (37-48 GB/s measured, whatever the tile), so below two 128x128 tiles per CU
 // a narrower tile spreads the same K over more CUs or more waves.  Measured
@@ -103,13 +105,18 @@ int match_fixed_chain(const fuseml_gemm_desc& d);
 // 1024x1024x1024 16.8 -> 9.9 on 32x128 tiles; 2048x1024x4096 44.7 -> 31.7,
 // 2048x2048x1024 20.0 -> 17.7 and 8192x512x2048 31.5 -> 28.8 on 64x128 tiles;
 // 2048x4096x1024 33.0 -> 29.0 and 4096x2048x1024 31.8 -> 29.5 on 256x128
-// ping-pong tiles (64x128 tiles there: 35.0 and 33.2).
+// ping-pong tiles (64x128 tiles there: 35.0 and 33.2); 128x32768x4096 stays on
+// 128x128 tiles (58.2; 64x128 63.8); 64x65536x4096 138.7 -> 125 and
+// 16x65536x1024 36.0 -> 23.0 on lock-step tiles instead of 256x256 ones.
 TileConfig choose_partial_round(const fuseml_gemm_desc& d, int cus) {
   struct Cand {
     const TileConfig* c;
     int w_one, w_two;  // weight with at most one / with two workgroups on a CU
   };
-  const Cand cand[4] = {{&kSmall, 8, 5}, {&kNarrow64, 8, 5}, {&kNarrow32, 8, 5}, {&kLarge128, 6, 6}};
+  // One lock-step workgroup per CU costs less beside a long K loop, where the
+  // pipeline runs in its steady state longer than the epilogue takes.
+  const int one = d.K > 2048 ? 7 : 8;
+  const Cand cand[4] = {{&kSmall, one, 5}, {&kNarrow64, one, 5}, {&kNarrow32, one, 5}, {&kLarge128, 6, 6}};
   const TileConfig* best = cand[0].c;
   int64_t best_work = 0;
   for (const Cand& k : cand) {
@@ -156,7 +163,7 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
   // one was 7-17% faster than 256x256 (bias+GELU at K = 512-1024), from 144
   // on the 256x256 ones are.
   const int64_t large_tiles = cdiv(d.M, 256) * cdiv(d.N, 256);
-  if (2 * large_tiles <= cus) return choose_partial_round(d, cus);
+  if (2 * large_tiles <= cus || d.M <= 128) return choose_partial_round(d, cus);
   if (d.K % 64 == 0 && (d.K >= 8192 || (d.K >= 2048 && large_tiles >= cus))) return kDeep3;
   if (d.K % 64 == 0 && d.K >= 1024 && large_tiles >= cus) {
     const int ch = match_fixed_chain(d);

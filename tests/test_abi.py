@@ -113,12 +113,16 @@ def test_tile_config_choice():
     ((128, 256, 1024), (32, 128, 4)),     # the reference's small preset's second GEMM: 8 tiles
     ((1, 4096, 1024), (32, 128, 4)),      # one row
     ((64, 512, 2048), (32, 128, 4)),
+    ((128, 32768, 4096), (128, 128, 4)),  # K > 2048: one 128x128 workgroup per CU beats two 64x128
+    ((64, 65536, 4096), (64, 128, 4)),    # M <= 128: no 256-row tiles even at a full round of them
+    ((16, 65536, 1024), (32, 128, 4)),
 ])
 def test_partial_round_tile_choice(shape, tile):
     """Below one round of 256x256 tiles the tile with the least K-loop work on
     its busiest CU: ceil(tiles / 256) x (BM + BN) operand rows, weighted 8:5
-    for a lock-step tile when no CU holds two workgroups and 6:5 for the
-    ping-pong tile, the first listed on a tie."""
+    (7:5 for K > 2048) for a lock-step tile when no CU holds two workgroups
+    and 6:5 for the ping-pong tile, the first listed on a tie; also for M <=
+    128 at any N."""
     lib = _abi.load_library()
     cfg = (ctypes.c_int32 * 4)()
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(*shape)), cfg) == 0

@@ -223,15 +223,18 @@ def test_partial_round_tile_mirrors_the_library():
 
     lib = _abi.load_library()
     cfg = (ctypes.c_int32 * 4)()
-    for M, N in ((1, 4096), (64, 512), (128, 256), (128, 1024), (512, 4096), (1000, 900), (1024, 1024),
-                 (2048, 1024), (2048, 2048), (2048, 4096)):
+    shapes = [(M, N, K) for M, N in ((1, 4096), (64, 512), (128, 256), (128, 1024), (512, 4096), (1000, 900),
+                                     (1024, 1024), (2048, 1024), (2048, 2048), (2048, 4096), (128, 32768),
+                                     (64, 65536), (16, 65536))
+              for K in (1024, 4096)]
+    for M, N, K in shapes:
         d = _abi.GemmDesc()
-        d.M, d.N, d.K = M, N, 1024
-        d.a, d.lda, d.b, d.ldb = 0x10000, 1024, 0x20000, 1024
+        d.M, d.N, d.K = M, N, K
+        d.a, d.lda, d.b, d.ldb = 0x10000, K, 0x20000, K
         d.ab_dtype = _abi.BF16
         d.out.ptr, d.out.ld, d.out.dtype = 0x30000, N, _abi.BF16
         assert lib.fuseml_gemm_epilogue_config(ctypes.byref(d), cfg) == 0, _abi.last_error(lib)
-        assert (cfg[0], cfg[1]) == comp.partial_round_tile(M, N)[0], (M, N)
+        assert (cfg[0], cfg[1]) == comp.partial_round_tile(M, N, K)[0], (M, N, K)
 
 
 class _TwoReductionChains(nn.Module):
