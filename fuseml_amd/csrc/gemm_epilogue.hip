@@ -97,10 +97,10 @@ int match_fixed_chain(const fuseml_gemm_desc& d);
 // CU, 8 with at most one (one wave per SIMD hides less of the LDS DMA's
 // latency and none of the epilogue; 7 for K > 2048), 6 for the ping-pong
 // tile; the first of the list on a tie.  Also for M <= 128 at any N, where a
-// 256-row tile is at least half padding.  Each
-// CU moves its tiles' A and W rows through the LDS DMA at a roughly fixed rate
-// (37-48 GB/s measured, whatever the tile), so below two 128x128 tiles per CU
-// a narrower tile spreads the same K over more CUs or more waves.  Measured
+// 256-row tile is at least half padding.  Each CU moves its tiles' A and W
+// rows through the LDS DMA at a roughly fixed rate (37-48 GB/s measured,
+// whatever the tile), so below two 128x128 tiles per CU a narrower tile
+// spreads the same K over more CUs or more waves.  Measured
 // (bias + GELU or bias + residual, M x N x K, us): 128x1024x256 9.6 -> 5.9 and
 // 1024x1024x1024 16.8 -> 9.9 on 32x128 tiles; 2048x1024x4096 44.7 -> 31.7,
 // 2048x2048x1024 20.0 -> 17.7 and 8192x512x2048 31.5 -> 28.8 on 64x128 tiles;
