@@ -217,6 +217,49 @@ def test_variant_chain_parity(forced_variant, chain, shape):
     _check_tile(out, ref, f"{forced_variant} {chain} {shape}")
 
 
+# The automatic tile choice on the device (its CU count): one shape per tile it
+# picks below a full round of 256x256 tiles, and a 64-row output with a full
+# round of them (M <= 128 runs on the smaller tiles).  The launched tile is
+# asserted through fuseml_gemm_epilogue_config, the output checked against
+# the oracle on two chains (one with a 2-D operand).
+AUTO_TILES = [
+    ((2048, 4096, 256), (256, 128, 8)),   # 256 ping-pong tiles: one round
+    ((2048, 1024, 256), (64, 128, 4)),
+    ((1000, 1000, 256), (32, 128, 4)),    # ragged M and N
+    ((128, 256, 1024), (32, 128, 4)),     # the reference's small preset's second GEMM
+    ((64, 65536, 256), (64, 128, 4)),     # a full round of 256x256 tiles at 64 rows
+    ((4096, 4096, 256), (256, 256, 8)),   # a full round: the 256x256 ping-pong kernel
+]
+
+
+@pytest.mark.parametrize("chain", ["bias_gelu", "bias_residual"])
+@pytest.mark.parametrize("shape,tile", AUTO_TILES, ids=lambda v: "x".join(map(str, v)))
+def test_automatic_tile_choice_parity(shape, tile, chain):
+    import ctypes
+
+    from fuseml_amd import _abi
+
+    M, N, K = shape
+    dtype = torch.bfloat16
+    a, w = _gemm_inputs(M, N, K, dtype, seed=31)
+    ops = _operands(M, N, dtype, seed=32)[:2]
+    inputs = ops + [a, w.t()]
+    left, right = len(ops), len(ops) + 1
+    steps = CHAINS[chain]
+    spec = _spec(left=left, right=right, ops=steps, out_dtype=dtype)
+    print(f"case automatic tile shape={shape} chain={chain}", flush=True)
+    L = _launcher(spec, len(inputs))
+    out = L(*[t.cuda() for t in inputs])
+    torch.cuda.synchronize()
+    (plan,) = L._plans.values()
+    cfg = (ctypes.c_int32 * 4)()
+    lib = _abi.load_library()
+    assert lib.fuseml_gemm_epilogue_config(plan.desc_ref, cfg) == 0, _abi.last_error(lib)
+    assert tuple(cfg[:3]) == tile, (shape, tuple(cfg[:3]))
+    ref = ora.gemm_epilogue([_np(t) for t in inputs], left, right, steps)["tile"]
+    _check_tile(out, ref, f"auto {shape} {chain}")
+
+
 # Fixed-chain kernels (compile-time epilogues of the deep3 variant) against the
 # generic op loop of the same variant: the same arithmetic in the same order,
 # so the outputs must be bitwise equal (sums and means, accumulated by fp32
