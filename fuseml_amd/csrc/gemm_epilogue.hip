@@ -106,8 +106,9 @@ int match_fixed_chain(const fuseml_gemm_desc& d);
 // 2048x2048x1024 20.0 -> 17.7 and 8192x512x2048 31.5 -> 28.8 on 64x128 tiles;
 // 2048x4096x1024 33.0 -> 29.0 and 4096x2048x1024 31.8 -> 29.5 on 256x128
 // ping-pong tiles (64x128 tiles there: 35.0 and 33.2); 128x32768x4096 stays on
-// 128x128 tiles (58.2; 64x128 63.8); 64x65536x4096 138.7 -> 125 and
-// 16x65536x1024 36.0 -> 23.0 on lock-step tiles instead of 256x256 ones.
+// 128x128 tiles (58.2; 64x128 63.8); 64x65536x4096 138.7 -> 125,
+// 16x65536x1024 36.0 -> 23.0, 128x65536x1024 38.7 -> 31.9 and 128x65536x4096
+// 151.9 -> 136.1 on lock-step tiles instead of 256x256 ones.
 TileConfig choose_partial_round(const fuseml_gemm_desc& d, int cus) {
   struct Cand {
     const TileConfig* c;
