@@ -256,7 +256,7 @@ def load_library() -> ctypes.CDLL:
         return lib
 
 
-VARIANTS = ("large", "deep", "deep3", "small", "narrow64", "narrow32", "large128")
+VARIANTS = ("large", "deep", "deep3", "small", "narrow64", "narrow32", "large128", "small64")
 
 
 def force_variant(name: Optional[str]) -> None:

@@ -75,7 +75,15 @@ PRESET_GROUPS: List[Tuple[str, str, int, int, int]] = [
     ("small G1", "bias_gelu", 128, 1024, 256),
     ("small G2", "bias_residual", 128, 256, 1024),
 ]
-GROUPS = CONFIG_GROUPS + K_SWEEP + FEW_TILES + PRESET_GROUPS
+# Decode-sized M against a wide weight (at least 512 128x128 output tiles):
+# both paths stream the weight from HBM once.
+DECODE: List[Tuple[str, str, int, int, int]] = [
+    ("decode 64x65536 K=4096", "bias_gelu", 64, 65536, 4096),
+    ("decode 128x65536 K=4096", "bias_residual", 128, 65536, 4096),
+    ("decode 128x65536 K=8192", "bias_gelu", 128, 65536, 8192),
+    ("decode 16x65536 K=2048", "bias_gelu", 16, 65536, 2048),
+]
+GROUPS = CONFIG_GROUPS + K_SWEEP + FEW_TILES + PRESET_GROUPS + DECODE
 
 # (M, D, I) MLP blocks (linear2(gelu(linear1(x))) + x) for the single-kernel
 # MLP's rule (``--mlp``): the reference's memory-bound widths over M, and C2.
@@ -152,7 +160,7 @@ def _median_ms(fn: Callable[[], object], iters: int) -> float:
 
 
 def measure(groups=GROUPS, passes: int = 2, dev: str = "cuda") -> List[Dict[str, object]]:
-    from .compiler import epilogue_passes, few_tile_verdict, fused_beats_eager
+    from .compiler import epilogue_passes, few_tile_verdict, fused_beats_eager, weight_streaming
     from .launcher import HipKernelLauncher
 
     rows = []
@@ -172,8 +180,8 @@ def measure(groups=GROUPS, passes: int = 2, dev: str = "cuda") -> List[Dict[str,
         tiles = -(-M // 128) * -(-N // 128)
         addmm = chain != "relu_3red"  # the other chains' GEMM is an addmm (bias in hipBLASLt's epilogue)
         p = epilogue_passes(spec, gemm_is_addmm=addmm)
-        few = few_tile_verdict(M, N, K) is not None
-        rule = (not few) and fused_beats_eager(spec, K, dtype=BF, gemm_is_addmm=addmm)[0]
+        few = few_tile_verdict(M, N, K) is not None and not weight_streaming(M, N)
+        rule = (not few) and fused_beats_eager(spec, K, dtype=BF, gemm_is_addmm=addmm, M=M, N=N)[0]
         rows.append({"group": label, "chain": chain, "M": M, "N": N, "K": K, "passes": p, "tiles_128": tiles,
                      "fused_ms": round(best["fused"], 4), "eager_ms": round(best["eager"], 4),
                      "mm_ms": round(best["mm"], 4), "fused_over_eager": round(best["fused"] / best["eager"], 3),

@@ -159,19 +159,43 @@ def device_is_gfx950(device: Optional[torch.device] = None) -> bool:
     return str(arch).startswith("gfx950")
 
 
-def _gemm_k(group: Any) -> Tuple[Optional[int], Any]:
-    """(K, dtype) of the group's GEMM from the left operand's metadata (K None
-    if unknown)."""
+def _gemm_dims(group: Any) -> Tuple[Optional[int], Any, Optional[int], Optional[int]]:
+    """(K, dtype, M, N) of the group's GEMM from its operands' metadata (None
+    where unknown)."""
     base = group.base_node
     args = (getattr(group, "node_args_snapshot", None) or {}).get(base.name, base.args)
-    mat1 = args[1] if base.target is TRIGGER_TARGETS[0] else args[0]
-    m = _meta(mat1)
+    addmm = base.target is TRIGGER_TARGETS[0]
+    mat1 = args[1] if addmm else args[0]
+    mat2 = args[2] if addmm else args[1]
+    m, w = _meta(mat1), _meta(mat2)
     if m is None or len(m.shape) != 2:
-        return None, None
+        return None, None, None, None
     try:
-        return int(m.shape[1]), getattr(m, "dtype", None)
+        K, M = int(m.shape[1]), int(m.shape[0])
     except (TypeError, ValueError):
-        return None, None
+        return None, None, None, None
+    N = None
+    if w is not None and len(w.shape) == 2:
+        try:
+            N = int(w.shape[1])
+        except (TypeError, ValueError):
+            N = None
+    return K, getattr(m, "dtype", None), M, N
+
+
+# Weight-streaming groups fuse while K <= this x elementwise passes
+# (profiles/cost_model_calibration.json, decode rows: one pass 0.85-0.97 of
+# eager's time at K = 2048-4096, 1.07 at K = 8192).
+WEIGHT_STREAM_K_PER_PASS = 4096
+
+
+def weight_streaming(M: int, N: int, cus: int = MI355X_CUS) -> bool:
+    """Decode-sized M against a wide weight: M <= 128 with at least one
+    128-column output tile per CU.  Both paths then stream the weight from HBM
+    once (the library runs one row of tiles, in K stages of 64), so the fused
+    kernel costs about eager's GEMM, saves its elementwise passes, and the
+    few-tile rule does not apply (fused_beats_eager decides)."""
+    return M <= 128 and -(-N // 128) >= cus
 
 
 def partial_round_tile(M: int, N: int, K: int, cus: int = MI355X_CUS) -> Tuple[Tuple[int, int], float]:
@@ -180,7 +204,12 @@ def partial_round_tile(M: int, N: int, K: int, cus: int = MI355X_CUS) -> Tuple[T
     unit of K: ceil(tiles / cus) x (BM + BN), weighted by how fast a CU moves
     them (a lock-step tile x 1.6 when no CU holds two workgroups, x 1.4 for K >
     2048; the ping-pong tile x 1.2); the least, the first listed on a tie
-    (choose_partial_round in csrc/gemm_epilogue.hip)."""
+    (choose_partial_round in csrc/gemm_epilogue.hip).  In the weight-streaming
+    regime (weight_streaming) the tile with the smallest BM >= M."""
+    if weight_streaming(M, N, cus):
+        bm = 32 if M <= 32 else 64 if M <= 64 else 128
+        tiles = -(-N // 128)
+        return (bm, 128), -(-tiles // cus) * (bm + 128) * (1.6 if tiles <= cus else 1.0)
     one = 7 if K > 2048 else 8
     best: Optional[Tuple[Tuple[int, int], int]] = None
     for bm, bn, lockstep in PARTIAL_ROUND_TILES:
@@ -227,7 +256,7 @@ def trigger_is_fusible(node: torch.fx.Node, min_output_elements: int = MIN_FUSIO
         return False, f"tiny output {M}x{N}"
     if K % 8 != 0 and m1.dtype != torch.float32:  # the fp32 split pads K
         return False, f"K={K} is not a multiple of 8"
-    why = few_tile_verdict(M, N, effective_k(K, m1.dtype), min_tiles_long_k)
+    why = None if weight_streaming(M, N) else few_tile_verdict(M, N, effective_k(K, m1.dtype), min_tiles_long_k)
     if why is not None:
         return False, f"K={K}, " + why
     return True, "fused"
@@ -310,7 +339,8 @@ def epilogue_passes(spec: EpilogueSpec, gemm_is_addmm: bool = True) -> int:
 
 def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOGUE_PASS,
                       dtype: Any = None, gemm_is_addmm: bool = True,
-                      k_offset: int = K_CROSSOVER_OFFSET) -> Tuple[bool, str]:
+                      k_offset: int = K_CROSSOVER_OFFSET, M: Optional[int] = None,
+                      N: Optional[int] = None) -> Tuple[bool, str]:
     """The fused kernel against eager (hipBLASLt GEMM + elementwise kernels).
 
     Measured on one MI355X by ``python -m fuseml_amd.calibration`` (each group
@@ -329,10 +359,17 @@ def fused_beats_eager(spec: EpilogueSpec, K: int, k_per_pass: int = K_PER_EPILOG
     5120 for two, 11264 for four); k_per_pass = 0 always fuses.
 
     fp32 groups always fuse: eager runs an fp32 GEMM at the fp32 MFMA rate
-    (157 TFLOP/s peak), the split product at a third of the bf16 rate."""
+    (157 TFLOP/s peak), the split product at a third of the bf16 rate.
+    Weight-streaming shapes (``M`` and ``N`` given, :func:`weight_streaming`)
+    fuse while K <= WEIGHT_STREAM_K_PER_PASS x passes."""
     if k_per_pass <= 0 or dtype == torch.float32:
         return True, "fused"
     passes = epilogue_passes(spec, gemm_is_addmm)
+    if M is not None and N is not None and weight_streaming(M, N):
+        if K <= WEIGHT_STREAM_K_PER_PASS * passes:
+            return True, "fused (decode-sized M: both paths stream the weight)"
+        return False, (f"K={K} with {passes} elementwise pass(es) at decode-sized M: eager's GEMM streams "
+                       f"the weight faster (fused iff K <= {WEIGHT_STREAM_K_PER_PASS} x passes)")
     limit = k_per_pass * passes - k_offset
     if K <= limit:
         return True, "fused"
@@ -521,9 +558,9 @@ class FuseMLCompiler:
                     logger.info("group %s stays eager: %s", group, exc)
                     spec = None
                 if spec is not None:
-                    K, ab_dtype = _gemm_k(group)
+                    K, ab_dtype, gM, gN = _gemm_dims(group)
                     addmm = group.base_node.target is TRIGGER_TARGETS[0]
-                    win, why = (fused_beats_eager(spec, K, self.k_per_epilogue_pass, ab_dtype, addmm)
+                    win, why = (fused_beats_eager(spec, K, self.k_per_epilogue_pass, ab_dtype, addmm, M=gM, N=gN)
                                 if K else (True, "fused"))
                     if not win:
                         logger.info("group %s stays eager: %s", group, why)

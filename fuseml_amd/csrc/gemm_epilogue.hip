@@ -60,12 +60,12 @@ constexpr int64_t kTileSpan = 256;  // largest tile edge of any variant
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Pinned variant: 0 automatic, else 1 + index into {large, deep, deep3, small,
-// deep3-generic, narrow64, narrow32, large128} (deep3-generic: deep3 with the
-// generic op loop even where a fixed chain matches).  Initialised once per process from FUSEML_HIP_TILE, changed
+// deep3-generic, narrow64, narrow32, large128, small64} (deep3-generic: deep3
+// with the generic op loop even where a fixed chain matches).  Initialised once per process from FUSEML_HIP_TILE, changed
 // only through fuseml_gemm_epilogue_force_variant.
 constexpr const char* kVariantNames[] = {"large", "deep", "deep3", "small", "deep3-generic", "narrow64", "narrow32",
-                                         "large128"};
-constexpr int kNumVariantNames = 8;
+                                         "large128", "small64"};
+constexpr int kNumVariantNames = 9;
 constexpr int kForcedDeep3Generic = 5;
 std::atomic<int> g_forced_variant{-1};  // -1: environment not read yet
 
@@ -145,6 +145,7 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
     case 6: return kNarrow64;
     case 7: return kNarrow32;
     case 8: return kLarge128;
+    case 9: return kSmall64;
     default: break;
   }
   // A 256x256 tile keeps the LDS traffic per MFMA low enough for the MFMA pipe
@@ -163,6 +164,14 @@ TileConfig choose_config(const fuseml_gemm_desc& d, int cus) {
   // tiles (choose_partial_round): at 128 large tiles on 256 CUs the 128x128
   // one was 7-17% faster than 256x256 (bias+GELU at K = 512-1024), from 144
   // on the 256x256 ones are.
+  // Decode-sized M against a wide weight (a 128-column tile per CU or more):
+  // the GEMM streams the weight from HBM, so one row of tiles (the smallest
+  // BM >= M: the weight read once) in K stages of 64 (128 contiguous bytes of
+  // each weight row per stage where 32 fetch 64).  128x65536x8192 251.9 ->
+  // 215.8 us and 128x32768x4096 59.6 -> 53.6 on the 128x128 tile at BK = 64
+  // instead of 32 (eager 219.9 and 57.3); 64 and 16 rows: 113.0 and 41.8 on
+  // 64x128 and 32x128 tiles (eager 134.2, 44.4).
+  if (d.M <= 128 && cdiv(d.N, 128) >= cus) return d.M <= 32 ? kNarrow32 : d.M <= 64 ? kNarrow64 : kSmall64;
   const int64_t large_tiles = cdiv(d.M, 256) * cdiv(d.N, 256);
   if (2 * large_tiles <= cus || d.M <= 128) return choose_partial_round(d, cus);
   if (d.K % 64 == 0 && (d.K >= 8192 || (d.K >= 2048 && large_tiles >= cus))) return kDeep3;
@@ -538,8 +547,8 @@ int fuseml_gemm_epilogue_force_variant(const char* name) {
   g_last_error[0] = '\0';
   const int v = variant_code(name);
   if (v < 0) {
-    set_error("unknown variant '%s' (large, deep, deep3, small, deep3-generic, narrow64, narrow32, large128 or auto)",
-              name);
+    set_error("unknown variant '%s' (large, deep, deep3, small, deep3-generic, narrow64, narrow32, large128, small64 "
+              "or auto)", name);
     return FUSEML_EINVAL;
   }
   forced_variant();  // the environment is read first, so it cannot override this later
@@ -606,6 +615,8 @@ int fuseml_gemm_epilogue(const fuseml_gemm_desc* desc, void* stream_ptr) {
     e = launch_variant<kLarge>(d, stream, cus);
   else if (c.sched == kDeep3.sched)
     e = launch_variant<kDeep3>(d, stream, cus);
+  else if (c.bm == kSmall64.bm && c.bk == kSmall64.bk)
+    e = launch_variant<kSmall64>(d, stream, 0);
   else if (c.bm == kNarrow64.bm)
     e = launch_variant<kNarrow64>(d, stream, 0);
   else if (c.bm == kNarrow32.bm)

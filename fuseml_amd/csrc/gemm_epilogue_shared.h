@@ -34,6 +34,7 @@ constexpr TileConfig kDeep3 = {256, 256, 64, 2, 2, 2, 6};  // as kDeep, whole-st
 constexpr TileConfig kNarrow64 = {64, 128, 64, 3, 2, 2, 0};  // 4 waves lock-step (wave tile 32x64), 74 KB LDS, 2 WG/CU
 constexpr TileConfig kNarrow32 = {32, 128, 64, 3, 1, 4, 0};  // 4 waves lock-step (wave tile 32x32), 62 KB LDS, 2 WG/CU
 constexpr TileConfig kLarge128 = {256, 128, 32, 4, 4, 2, 1};  // 8 waves ping-pong (wave tile 64x64), 100 KB LDS, 1 WG/CU
+constexpr TileConfig kSmall64 = {128, 128, 64, 4, 2, 2, 0};  // kSmall at BK = 64: 130 KB LDS, 1 WG/CU
 
 // Epilogue chains compiled into kernels of their own (template parameter CH
 // of the kernel).  kChainGeneric runs the descriptor's op list through the

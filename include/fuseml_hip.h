@@ -174,7 +174,8 @@ int fuseml_gemm_epilogue_chain(const fuseml_gemm_desc* desc);
  * with whole-stage fragments; K % 64 == 0, else deep), "deep3-generic"
  * (deep3 with the generic op loop even where a fixed chain matches), "small"
  * (128x128), "narrow64" (64x128), "narrow32" (32x128), "large128" (256x128
- * ping-pong), or NULL / "" / "auto" for the automatic choice.  The environment variable
+ * ping-pong), "small64" (128x128 at BK = 64), or NULL / "" / "auto" for the
+ * automatic choice.  The environment variable
  * FUSEML_HIP_TILE sets the initial value; it is read once per process.  For
  * tuning sweeps and per-variant parity tests; it replaces pinning a Triton
  * autotune config (fuseml/codegen/kernel_generator.py:587-615).  Returns

@@ -113,9 +113,9 @@ def test_tile_config_choice():
     ((128, 256, 1024), (32, 128, 4)),     # the reference's small preset's second GEMM: 8 tiles
     ((1, 4096, 1024), (32, 128, 4)),      # one row
     ((64, 512, 2048), (32, 128, 4)),
-    ((128, 32768, 4096), (128, 128, 4)),  # K > 2048: one 128x128 workgroup per CU beats two 64x128
-    ((64, 65536, 4096), (64, 128, 4)),    # M <= 128: no 256-row tiles even at a full round of them
-    ((16, 65536, 1024), (32, 128, 4)),
+    ((2048, 1024, 8192), (64, 128, 4)),   # K > 2048: one 64x128 workgroup per CU (192 rows x 1.4)
+    ((128, 16384, 4096), (64, 128, 4)),   # 128 column tiles, fewer than one per CU: not weight streaming
+    ((128, 8192, 1024), (32, 128, 4)),
 ])
 def test_partial_round_tile_choice(shape, tile):
     """Below one round of 256x256 tiles the tile with the least K-loop work on
@@ -128,6 +128,24 @@ def test_partial_round_tile_choice(shape, tile):
     assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(*shape)), cfg) == 0
     assert tuple(cfg[:3]) == tile
     assert cfg[3] <= 160 * 1024 and (tile[2] == 8 or 2 * cfg[3] <= 160 * 1024)
+
+
+@pytest.mark.parametrize("shape,tile", [
+    ((128, 32768, 4096), (128, 128)),  # 65-128 rows: the 128x128 tile at BK = 64
+    ((96, 65536, 1024), (128, 128)),
+    ((64, 65536, 4096), (64, 128)),    # 33-64 rows
+    ((16, 65536, 1024), (32, 128)),    # up to 32 rows
+])
+def test_weight_streaming_tile_choice(shape, tile):
+    """M <= 128 with a 128-column tile per CU or more: one row of tiles, the
+    smallest BM >= M, so the weight is read once; 128 rows in K stages of 64
+    (130 KB of LDS: one workgroup per CU)."""
+    lib = _abi.load_library()
+    cfg = (ctypes.c_int32 * 4)()
+    assert lib.fuseml_gemm_epilogue_config(ctypes.byref(_desc(*shape)), cfg) == 0
+    assert (cfg[0], cfg[1], cfg[2]) == (*tile, 4)
+    if tile == (128, 128):
+        assert 128 * 1024 < cfg[3] <= 160 * 1024
 
 
 def test_force_variant_pins_and_releases():

@@ -212,6 +212,26 @@ def test_cost_model_few_tiles_long_k():
     assert trigger_is_fusible(node(1024, 1024, 1024))[0]
     # the reference's medium preset's second GEMM (128 tiles, 64x128 tiles, K = 4096) stays eager
     assert not trigger_is_fusible(node(2048, 4096, 1024))[0]
+    # decode-sized M against a wide weight streams the weight either way: no few-tile objection
+    assert trigger_is_fusible(node(128, 8192, 32768))[0] and trigger_is_fusible(node(16, 4096, 65536))[0]
+    assert not trigger_is_fusible(node(128, 8192, 16384))[0]   # 128 column tiles: fewer than one per CU
+
+
+def test_weight_streaming_groups_fuse_to_4096_per_pass():
+    """fused_beats_eager: with M and N given, M <= 128 and a 128-column tile
+    per CU fuse while K <= 4096 x passes (one pass: 4096, where the pass rule
+    stops at 2048); without them, or at M = 129, the pass rule."""
+    from fuseml_amd.epilogue import EpilogueSpec, EpiOp
+
+    spec = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("gelu_erf")), BF)
+    assert not comp.fused_beats_eager(spec, 4096)[0]
+    assert comp.fused_beats_eager(spec, 4096, M=128, N=65536)[0]
+    assert not comp.fused_beats_eager(spec, 8192, M=128, N=65536)[0]
+    assert not comp.fused_beats_eager(spec, 4096, M=129, N=65536)[0]
+    assert not comp.fused_beats_eager(spec, 4096, M=128, N=16384)[0]
+    two = EpilogueSpec(1, 2, (EpiOp("add", 0), EpiOp("gelu_erf"), EpiOp("add", 3)), BF)
+    assert comp.fused_beats_eager(two, 8192, M=64, N=65536)[0]
+    assert comp.weight_streaming(1, 32768) and not comp.weight_streaming(1, 32640)
 
 
 def test_partial_round_tile_mirrors_the_library():
@@ -224,8 +244,8 @@ def test_partial_round_tile_mirrors_the_library():
     lib = _abi.load_library()
     cfg = (ctypes.c_int32 * 4)()
     shapes = [(M, N, K) for M, N in ((1, 4096), (64, 512), (128, 256), (128, 1024), (512, 4096), (1000, 900),
-                                     (1024, 1024), (2048, 1024), (2048, 2048), (2048, 4096), (128, 32768),
-                                     (64, 65536), (16, 65536))
+                                     (1024, 1024), (2048, 1024), (2048, 2048), (2048, 4096), (128, 16384),
+                                     (128, 32768), (96, 65536), (64, 65536), (16, 65536))
               for K in (1024, 4096)]
     for M, N, K in shapes:
         d = _abi.GemmDesc()

@@ -20,7 +20,8 @@ import pytest
 import torch
 
 from fuseml_amd import calibration as cal
-from fuseml_amd.compiler import MIN_TILES_LONG_K, epilogue_passes, few_tile_verdict, fused_beats_eager
+from fuseml_amd.compiler import (MIN_TILES_LONG_K, epilogue_passes, few_tile_verdict, fused_beats_eager,
+                                 weight_streaming)
 from fuseml_amd.mlp import mlp_block_beats_two_launches
 
 PROFILES = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "profiles")
@@ -48,9 +49,9 @@ def _rows():
 def _decision(row):
     spec, _ = cal._spec(row["chain"])
     addmm = row["chain"] != "relu_3red"
-    if few_tile_verdict(row["M"], row["N"], row["K"]) is not None:
+    if few_tile_verdict(row["M"], row["N"], row["K"]) is not None and not weight_streaming(row["M"], row["N"]):
         return False
-    return fused_beats_eager(spec, row["K"], dtype=torch.bfloat16, gemm_is_addmm=addmm)[0]
+    return fused_beats_eager(spec, row["K"], dtype=torch.bfloat16, gemm_is_addmm=addmm, M=row["M"], N=row["N"])[0]
 
 
 def test_calibration_covers_the_config_groups_and_both_rules():

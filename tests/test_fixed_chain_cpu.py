@@ -81,7 +81,7 @@ def test_each_fixed_chain_is_matched(lib, name):
 @pytest.mark.parametrize("name", sorted(CASES))
 def test_generic_pin_and_other_variants_keep_the_op_loop(lib, name):
     chain, _ = CASES[name]
-    for variant in ("deep3-generic", "large", "deep", "small", "narrow64", "narrow32", "large128"):
+    for variant in ("deep3-generic", "large", "deep", "small", "narrow64", "narrow32", "large128", "small64"):
         assert _chain(lib, _ops(_desc(), chain), variant) == 0, variant
 
 

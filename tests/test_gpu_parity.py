@@ -168,7 +168,7 @@ def test_reductions_parity(axis, shape):
 # schedules on every chain, on ragged edges and on K that ends mid-stage.
 # ---------------------------------------------------------------------------
 
-VARIANTS = ["large", "deep", "deep3", "deep3-generic", "small", "narrow64", "narrow32", "large128"]
+VARIANTS = ["large", "deep", "deep3", "deep3-generic", "small", "narrow64", "narrow32", "large128", "small64"]
 
 
 def _k_for(variant, K):
@@ -227,7 +227,8 @@ AUTO_TILES = [
     ((2048, 1024, 256), (64, 128, 4)),
     ((1000, 1000, 256), (32, 128, 4)),    # ragged M and N
     ((128, 256, 1024), (32, 128, 4)),     # the reference's small preset's second GEMM
-    ((64, 65536, 256), (64, 128, 4)),     # a full round of 256x256 tiles at 64 rows
+    ((64, 65536, 256), (64, 128, 4)),     # 64 rows against a wide weight: one row of 64x128 tiles
+    ((100, 33000, 264), (128, 128, 4)),   # 100 rows: one row of 128x128 tiles at BK = 64, ragged N and K
     ((4096, 4096, 256), (256, 256, 8)),   # a full round: the 256x256 ping-pong kernel
 ]
 
